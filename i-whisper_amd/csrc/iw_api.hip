@@ -1,0 +1,481 @@
+// C ABI entry points (include/iwhisper_amd.h): argument checks, then launch.
+#include "../../include/iwhisper_amd.h"
+#include "iw_common.hpp"
+#include "iw_gemm.hpp"
+#include "iw_kernels.hpp"
+
+#include <string>
+
+namespace iw {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const std::string &msg) { g_last_error = msg; }
+
+int fail(const std::string &msg) {
+  g_last_error = msg;
+  return IW_EINVAL;
+}
+
+int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return IW_ELAUNCH;
+  }
+  return IW_OK;
+}
+
+namespace {
+
+hipStream_t as_stream(iw_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+GemmArgs linear_args(const int8_t *x, const int8_t *w, const int32_t *bias, const int8_t *wz,
+                     const uint32_t *mult, const int8_t *shift, void *out, int64_t M, int64_t K,
+                     int64_t N, bool has_bias, bool asym, int epi) {
+  GemmArgs g;
+  g.a = x;
+  g.lda = K;
+  g.b = w;
+  g.ldb = K;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.epi = epi;
+  g.bias = has_bias ? bias : nullptr;
+  g.wz = asym ? wz : nullptr;
+  g.mult = mult;
+  g.shift = shift;
+  g.mult_pc = 1;
+  g.out = out;
+  g.ldc = N;
+  return g;
+}
+
+int check_linear(const void *x, const void *w, const int32_t *bias, const int8_t *wz,
+                 const void *mult, const void *shift, const void *out, int64_t M, int64_t K,
+                 int64_t N, bool has_bias, bool asym) {
+  IW_REQUIRE(M >= 0 && N > 0, "invalid GEMM shape");
+  IW_REQUIRE(K > 0, "x.size(-1) must be greater than 0");
+  IW_REQUIRE(M == 0 || (x && w && mult && shift && out), "null tensor pointer");
+  IW_REQUIRE(!has_bias || bias, "has_bias set but bias is null");
+  IW_REQUIRE(!asym || wz, "asymmetric set but weight_zero is null");
+  return IW_OK;
+}
+
+int check_gelu_counts(int64_t channels, int64_t luti_count, int64_t luto_count) {
+  IW_REQUIRE(luti_count == 1 || luti_count == channels,
+             "luti parameters must be scalar or match input.size(-1)");
+  IW_REQUIRE(luto_count == 1 || luto_count == channels,
+             "luto parameters must be scalar or match input.size(-1)");
+  return IW_OK;
+}
+
+}  // namespace
+}  // namespace iw
+
+using namespace iw;
+
+extern "C" {
+
+int iw_abi_version(void) { return IW_ABI_VERSION; }
+
+const char *iw_last_error(void) { return g_last_error.c_str(); }
+
+int iw_linear8(const int8_t *x, const int8_t *weight, const int32_t *bias,
+               const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+               int8_t *out, int64_t M, int64_t K, int64_t N, bool has_bias, bool asymmetric,
+               iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias,
+                        asymmetric);
+  if (rc) return rc;
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N,
+                           has_bias, asymmetric, EPI_L8);
+  return gemm_dense(g, as_stream(stream));
+}
+
+int iw_linear8_gelu(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                    const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                    const uint8_t *lut, const uint8_t *luti_multiplier, const int8_t *luti_shift,
+                    const uint8_t *luto_multiplier, const int8_t *luto_shift, int64_t luti_count,
+                    int64_t luto_count, int8_t *out, int64_t M, int64_t K, int64_t N,
+                    bool has_bias, bool asymmetric, iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias,
+                        asymmetric);
+  if (rc) return rc;
+  rc = check_gelu_counts(N, luti_count, luto_count);
+  if (rc) return rc;
+  IW_REQUIRE(lut && luti_multiplier && luti_shift && luto_multiplier && luto_shift,
+             "null GeLU parameter pointer");
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N,
+                           has_bias, asymmetric, EPI_L8);
+  g.lut = lut;
+  g.luti_m = luti_multiplier;
+  g.luti_s = luti_shift;
+  g.luto_m = luto_multiplier;
+  g.luto_s = luto_shift;
+  g.luti_pc = luti_count != 1;
+  g.luto_pc = luto_count != 1;
+  return gemm_dense(g, as_stream(stream));
+}
+
+int iw_linear32(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                int32_t *out, int64_t M, int64_t K, int64_t N, bool has_bias, bool asymmetric,
+                iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias,
+                        asymmetric);
+  if (rc) return rc;
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N,
+                           has_bias, asymmetric, EPI_L32);
+  return gemm_dense(g, as_stream(stream));
+}
+
+int iw_linear32_residual15(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                           const int8_t *weight_zero, const uint32_t *multiplier,
+                           const int8_t *shift, const int16_t *residual,
+                           uint16_t residual_multiplier, int16_t *out, int64_t M, int64_t K,
+                           int64_t N, bool has_bias, bool asymmetric, iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias,
+                        asymmetric);
+  if (rc) return rc;
+  IW_REQUIRE(M == 0 || residual, "null residual pointer");
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N,
+                           has_bias, asymmetric, EPI_L32RES);
+  g.res = residual;
+  g.ldres = N;
+  g.res_mult = residual_multiplier;
+  return gemm_dense(g, as_stream(stream));
+}
+
+int iw_classifier(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift,
+                  int8_t *out, int64_t M, int64_t K, int64_t N, iw_stream_t stream) {
+  IW_REQUIRE(K > 0, "hidden size must be positive");
+  IW_REQUIRE(N > 0, "vocabulary size must be positive");
+  IW_REQUIRE(M >= 0, "invalid row count");
+  if (M == 0) return IW_OK;
+  IW_REQUIRE(x && weight && out, "null tensor pointer");
+  GemmArgs g;
+  g.a = x;
+  g.lda = K;
+  g.b = weight;
+  g.ldb = K;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.epi = EPI_S8;
+  g.mult_pc = 0;
+  g.out = out;
+  g.ldc = N;
+  g.scalar_mult = multiplier;
+  g.scalar_shift = shift;
+  return gemm_dense(g, as_stream(stream));
+}
+
+int iw_layernorm32(const int16_t *x, const int8_t *weight, const int32_t *bias,
+                   uint8_t ln_multiplier, int8_t ln_shift, uint32_t out_multiplier,
+                   int8_t out_shift, uint32_t rsqrt_offset, int8_t *out, int64_t rows,
+                   int64_t hidden, bool has_bias, iw_stream_t stream) {
+  IW_REQUIRE(layernorm_width_code(hidden) >= 0,
+             "unsupported LayerNorm hidden size: " + std::to_string(hidden));
+  IW_REQUIRE(rows >= 0, "invalid row count");
+  if (rows == 0) return IW_OK;
+  IW_REQUIRE(x && weight && out, "null tensor pointer");
+  IW_REQUIRE(!has_bias || bias, "has_bias set but bias is null");
+  IW_REQUIRE((reinterpret_cast<uintptr_t>(x) & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+             "LayerNorm input must be 8-byte and output 4-byte aligned");
+  return launch_layernorm32(x, weight, has_bias ? bias : nullptr, ln_multiplier, ln_shift,
+                            out_multiplier, out_shift, rsqrt_offset, out, rows, hidden,
+                            as_stream(stream));
+}
+
+int iw_layernorm32_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t offset,
+                         iw_stream_t stream) {
+  IW_REQUIRE(n >= 0, "invalid element count");
+  IW_REQUIRE(n == 0 || (x && out), "null tensor pointer");
+  IW_REQUIRE(offset <= 29, "rsqrt_offset must be in [0,29]");
+  return launch_rsqrt(x, out, n, offset, as_stream(stream));
+}
+
+int iw_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_multiplier,
+            const int8_t *luti_shift, const uint8_t *luto_multiplier, const int8_t *luto_shift,
+            int8_t *out, int64_t numel, int64_t channels, int64_t luti_count,
+            int64_t luto_count, iw_stream_t stream) {
+  IW_REQUIRE(numel >= 0 && channels > 0 && numel % channels == 0, "invalid GeLU shape");
+  int rc = check_gelu_counts(channels, luti_count, luto_count);
+  if (rc) return rc;
+  if (numel == 0) return IW_OK;
+  IW_REQUIRE(x && lut && luti_multiplier && luti_shift && luto_multiplier && luto_shift && out,
+             "null tensor pointer");
+  return launch_gelu(x, lut, luti_multiplier, luti_shift, luto_multiplier, luto_shift, out, numel,
+                     channels, luti_count != 1, luto_count != 1, as_stream(stream));
+}
+
+int iw_residual15(const int32_t *branch, const int16_t *residual, uint16_t multiplier,
+                  int16_t *out, int64_t numel, iw_stream_t stream) {
+  IW_REQUIRE(numel >= 0, "invalid element count");
+  IW_REQUIRE(numel == 0 || (branch && residual && out), "null tensor pointer");
+  return launch_residual15(branch, residual, multiplier, out, numel, as_stream(stream));
+}
+
+int iw_add_requant15(const int8_t *x, const int8_t *addend, const uint16_t *multiplier,
+                     const int8_t *shift, int16_t *out, int64_t batch, int64_t positions,
+                     int64_t channels, int64_t multiplier_count, int64_t shift_count,
+                     iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && positions >= 0 && channels > 0, "invalid add_requant15 shape");
+  IW_REQUIRE(multiplier_count == 1 || multiplier_count == channels,
+             "multiplier must contain 1 or C elements");
+  IW_REQUIRE(shift_count == 1 || shift_count == channels, "shift must contain 1 or C elements");
+  if (batch * positions == 0) return IW_OK;
+  IW_REQUIRE(x && addend && multiplier && shift && out, "null tensor pointer");
+  return launch_add_requant15(x, nullptr, addend, multiplier, shift, out, batch, positions,
+                              channels, multiplier_count != 1, shift_count != 1,
+                              as_stream(stream));
+}
+
+int iw_embed_add_requant15(const int64_t *tokens, const int8_t *table, const int8_t *pe,
+                           int64_t offset, const uint16_t *multiplier, const int8_t *shift,
+                           int16_t *out, int64_t batch, int64_t positions, int64_t channels,
+                           iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && positions >= 0 && channels > 0 && offset >= 0,
+             "invalid embedding shape");
+  if (batch * positions == 0) return IW_OK;
+  IW_REQUIRE(tokens && table && pe && multiplier && shift && out, "null tensor pointer");
+  return launch_add_requant15(table, tokens, pe + offset * channels, multiplier, shift, out, batch,
+                              positions, channels, 0, 0, as_stream(stream));
+}
+
+int iw_conv1d(const int8_t *x, const int8_t *weight, const int32_t *bias, uint32_t multiplier,
+              int8_t shift, int8_t *out, int64_t batch, int64_t in_channels,
+              int64_t input_length, int64_t out_channels, int64_t kernel_size, int64_t stride,
+              int64_t padding, bool has_bias, iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && in_channels > 0 && out_channels > 0 && kernel_size > 0,
+             "invalid conv1d shape");
+  IW_REQUIRE(stride > 0, "stride must be positive");
+  IW_REQUIRE(padding >= 0, "padding must be non-negative");
+  const int64_t tout = (input_length + 2 * padding - kernel_size) / stride + 1;
+  IW_REQUIRE(input_length + 2 * padding >= kernel_size, "input too short for the kernel");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(x && weight && out, "null tensor pointer");
+  IW_REQUIRE(!has_bias || bias, "has_bias set but bias is null");
+  GemmArgs g;
+  g.a = x;
+  g.conv_tin = input_length;
+  g.conv_cin = in_channels;
+  g.conv_stride = stride;
+  g.conv_pad = padding;
+  g.conv_tout = tout;
+  g.conv_ksize = kernel_size;
+  g.b = weight;
+  g.ldb = in_channels * kernel_size;
+  g.M = batch * tout;
+  g.N = out_channels;
+  g.K = in_channels * kernel_size;
+  g.epi = EPI_S8;
+  g.bias = has_bias ? bias : nullptr;
+  g.mult_pc = 0;
+  g.scalar_mult = multiplier;
+  g.scalar_shift = shift;
+  g.out = out;
+  g.out_T = tout;
+  return gemm_conv(g, false, as_stream(stream));
+}
+
+int iw_conv1d_cl(const int8_t *x, const int8_t *weight_kc, const int32_t *bias,
+                 uint32_t multiplier, int8_t shift, const uint8_t *lut,
+                 const uint8_t *luti_multiplier, const int8_t *luti_shift,
+                 const uint8_t *luto_multiplier, const int8_t *luto_shift, int64_t luti_count,
+                 int64_t luto_count, const int8_t *pe, const uint16_t *pe_multiplier,
+                 const int8_t *pe_shift, int64_t pe_multiplier_count, int64_t pe_shift_count,
+                 void *out, int64_t batch, int64_t in_channels, int64_t input_length,
+                 int64_t out_channels, int64_t kernel_size, int64_t stride, int64_t padding,
+                 bool has_bias, iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && in_channels > 0 && out_channels > 0 && kernel_size > 0 && stride > 0 &&
+                 padding >= 0 && input_length + 2 * padding >= kernel_size,
+             "invalid conv1d shape");
+  IW_REQUIRE(in_channels % 16 == 0, "channels-last conv needs in_channels % 16 == 0");
+  int rc = check_gelu_counts(out_channels, luti_count, luto_count);
+  if (rc) return rc;
+  const int64_t tout = (input_length + 2 * padding - kernel_size) / stride + 1;
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(x && weight_kc && out && lut && luti_multiplier && luti_shift && luto_multiplier &&
+                 luto_shift,
+             "null tensor pointer");
+  IW_REQUIRE(!has_bias || bias, "has_bias set but bias is null");
+  GemmArgs g;
+  g.a = x;
+  g.conv_tin = input_length;
+  g.conv_cin = in_channels;
+  g.conv_stride = stride;
+  g.conv_pad = padding;
+  g.conv_tout = tout;
+  g.conv_ksize = kernel_size;
+  g.b = weight_kc;
+  g.ldb = in_channels * kernel_size;
+  g.M = batch * tout;
+  g.N = out_channels;
+  g.K = in_channels * kernel_size;
+  g.epi = EPI_S8;
+  g.bias = has_bias ? bias : nullptr;
+  g.mult_pc = 0;
+  g.scalar_mult = multiplier;
+  g.scalar_shift = shift;
+  g.lut = lut;
+  g.luti_m = luti_multiplier;
+  g.luti_s = luti_shift;
+  g.luto_m = luto_multiplier;
+  g.luto_s = luto_shift;
+  g.luti_pc = luti_count != 1;
+  g.luto_pc = luto_count != 1;
+  if (pe) {
+    IW_REQUIRE(pe_multiplier && pe_shift, "null positional requant parameters");
+    IW_REQUIRE(pe_multiplier_count == 1 || pe_multiplier_count == out_channels,
+               "multiplier must contain 1 or C elements");
+    IW_REQUIRE(pe_shift_count == 1 || pe_shift_count == out_channels,
+               "shift must contain 1 or C elements");
+    g.pe = pe;
+    g.pe_mult = pe_multiplier;
+    g.pe_shift = pe_shift;
+    g.pe_mpc = pe_multiplier_count != 1;
+    g.pe_spc = pe_shift_count != 1;
+    g.pe_T = tout;
+  }
+  g.out = out;
+  g.ldc = out_channels;
+  return gemm_conv(g, true, as_stream(stream));
+}
+
+int iw_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t batch, int64_t n_mels,
+                    int64_t frames, iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && n_mels > 0 && frames > 0, "invalid mel shape");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(mel && out, "null tensor pointer");
+  return launch_quantize_mel(mel, alpha, out, batch, n_mels, frames, as_stream(stream));
+}
+
+int iw_qk_requant_rowmax(const int8_t *q, const int8_t *k, const bool *mask, int16_t *qk,
+                         int16_t *row_max_plus1, int64_t batch, int64_t heads, int64_t q_length,
+                         int64_t k_length, int64_t head_dim, uint8_t multiplier, int32_t shift,
+                         bool has_mask, iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && heads >= 0 && q_length >= 0 && k_length >= 0 && head_dim >= 0,
+             "invalid attention shape");
+  if (batch * heads * q_length == 0) return IW_OK;
+  IW_REQUIRE(q && k && qk && row_max_plus1, "null tensor pointer");
+  IW_REQUIRE(!has_mask || mask, "has_mask set but mask is null");
+  return launch_qk_requant_rowmax(q, k, has_mask ? reinterpret_cast<const uint8_t *>(mask) : nullptr,
+                                  qk, row_max_plus1, batch * heads, q_length, k_length, head_dim,
+                                  multiplier, shift, as_stream(stream));
+}
+
+int iw_shift_exp(const int16_t *qk, const int16_t *row_max_plus1, const bool *mask, uint8_t *p,
+                 int32_t *row_sum, int64_t batch, int64_t heads, int64_t q_length,
+                 int64_t k_length, int32_t frac_bits, bool has_mask, iw_stream_t stream) {
+  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
+  IW_REQUIRE(batch >= 0 && heads >= 0 && q_length >= 0 && k_length >= 0,
+             "invalid attention shape");
+  if (batch * heads * q_length == 0) return IW_OK;
+  IW_REQUIRE(qk && row_max_plus1 && p && row_sum, "null tensor pointer");
+  IW_REQUIRE(!has_mask || mask, "has_mask set but mask is null");
+  return launch_shift_exp(qk, row_max_plus1,
+                          has_mask ? reinterpret_cast<const uint8_t *>(mask) : nullptr, p, row_sum,
+                          batch * heads, q_length, k_length, frac_bits, as_stream(stream));
+}
+
+int iw_pv_norm_requant(const uint8_t *p, const int8_t *v, const int32_t *row_sum,
+                       uint8_t av_multiplier, int8_t av_shift, uint32_t rsqrt_offset,
+                       int8_t *out, int64_t batch, int64_t heads, int64_t q_length,
+                       int64_t k_length, int64_t head_dim, iw_stream_t stream) {
+  IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
+  IW_REQUIRE(batch >= 0 && heads >= 0 && q_length >= 0 && k_length >= 0 && head_dim >= 0,
+             "invalid attention shape");
+  if (batch * heads * q_length * head_dim == 0) return IW_OK;
+  IW_REQUIRE(p && v && row_sum && out, "null tensor pointer");
+  return launch_pv_norm_requant(p, v, row_sum, av_multiplier, av_shift, rsqrt_offset, out, batch,
+                                heads, q_length, k_length, head_dim, as_stream(stream));
+}
+
+int iw_shift_exp_table(uint8_t *table, int32_t frac_bits, iw_stream_t stream) {
+  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
+  IW_REQUIRE(table, "null table pointer");
+  return launch_shift_exp_lut(table, frac_bits, as_stream(stream));
+}
+
+int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, int64_t k_sb,
+                 int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb, int64_t v_sh,
+                 int64_t v_sd, int8_t *out, int64_t o_sb, int64_t o_st, const bool *mask,
+                 int64_t batch, int64_t heads, int64_t q_length, int64_t k_length,
+                 int64_t head_dim, uint8_t qk_multiplier, int8_t qk_shift, int32_t frac_bits,
+                 uint8_t av_multiplier, int8_t av_shift, uint32_t rsqrt_offset,
+                 const uint8_t *table, bool decode, iw_stream_t stream) {
+  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
+  IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
+  IW_REQUIRE(head_dim > 0 && head_dim <= 128 && head_dim % 16 == 0,
+             "fused attention needs head_dim % 16 == 0 and head_dim <= 128");
+  IW_REQUIRE(batch >= 0 && heads > 0 && q_length >= 0 && k_length >= 0, "invalid attention shape");
+  IW_REQUIRE(batch <= 0x7fffffff && q_length <= 0x7fffffff && k_length <= 0x7fffffff,
+             "attention shape too large");
+  if (batch * q_length == 0) return IW_OK;
+  IW_REQUIRE(q && k && vt && out, "null tensor pointer");
+  IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((k_length + 15) / 16) * 16,
+             "transposed V rows must be 16-byte multiples covering k_length");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(vt) | (uintptr_t)q_sb | (uintptr_t)q_st |
+                          (uintptr_t)k_sb | (uintptr_t)k_sh | (uintptr_t)k_st | (uintptr_t)v_sb |
+                          (uintptr_t)v_sh;
+  IW_REQUIRE((align & 15) == 0, "fused attention operands must be 16-byte aligned");
+  AttnArgs a;
+  a.q = q;
+  a.q_sb = q_sb;
+  a.q_st = q_st;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_st = k_st;
+  a.vt = vt;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sd = v_sd;
+  a.vt_ld = v_sd;
+  a.out = out;
+  a.o_sb = o_sb;
+  a.o_st = o_st;
+  a.mask = reinterpret_cast<const uint8_t *>(mask);
+  a.B = (int32_t)batch;
+  a.H = (int32_t)heads;
+  a.Tq = (int32_t)q_length;
+  a.Tk = (int32_t)k_length;
+  a.D = (int32_t)head_dim;
+  a.qk_m = qk_multiplier;
+  a.qk_s = (uint32_t)(qk_shift > 0 ? qk_shift : 0);
+  a.frac_bits = frac_bits;
+  a.av_m = av_multiplier;
+  a.av_s = (uint32_t)(av_shift < 0 ? 0 : (av_shift > 32 ? 32 : av_shift));
+  a.rsqrt_off = rsqrt_offset;
+  a.lut = table;
+  if (decode) {
+    IW_REQUIRE(q_length <= 8, "decode attention handles at most 8 query rows");
+    return launch_attn_decode(a, as_stream(stream));
+  }
+  IW_REQUIRE(table, "prefill attention needs the shift-exp table");
+  IW_REQUIRE(v_sh == head_dim * v_sd && v_sb == heads * head_dim * v_sd && k_sh == head_dim,
+             "prefill attention expects V^T as [B,H,D,v_sd] and K as [B,T,H*D]");
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      cus = v;
+  }
+  return launch_attn_prefill(a, cus * 3, as_stream(stream));
+}
+
+int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
+                   iw_stream_t stream) {
+  IW_REQUIRE(rows >= 0 && cols > 0 && ld >= cols, "invalid argmax shape");
+  if (rows == 0) return IW_OK;
+  IW_REQUIRE(x && out, "null tensor pointer");
+  return launch_argmax_rows(x, rows, cols, ld, out, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,510 @@
+// Integer attention on gfx950.
+//
+// Op-level kernels, one per reference op (attention/attention_scalar.cpp):
+//   qk_requant_rowmax  :216-334   QK^T, requant to int16, masked row max + 1
+//   shift_exp          :388-568   shift-exponential to uint8 P and int32 row sums
+//   pv_norm_requant    :676-814   P.V, FISR normalisation, AV requant, [B,Tq,H*D]
+//
+// Fused kernels used by the layer API (bit-identical to the three ops above):
+//   attn_prefill  - MFMA kernel for long query blocks (encoder self-attention,
+//                   decoder prompt). Two passes over K: pass 1 takes the row max
+//                   of the raw int32 scores (the requant is monotone, so
+//                   requant(max) == max(requant)); pass 2 recomputes the scores,
+//                   maps them to P through a per-launch shift-exp table in LDS,
+//                   and accumulates P.V on MFMA. The int16 score and uint8 P
+//                   tensors are never written to memory.
+//   attn_decode   - streaming kernel for a few query rows over a KV cache
+//                   (decoder self- and cross-attention).
+#include "iw_common.hpp"
+#include "iw_kernels.hpp"
+
+namespace iw {
+
+namespace {
+
+__device__ __forceinline__ int32_t qk_requant16(int32_t acc, uint32_t m, uint32_t s) {
+  // (int32)(acc * m) modulo 2^32, Rshift, saturate to int16
+  return clampi(rshift((int32_t)((uint32_t)acc * m), s), -32768, 32767);
+}
+
+// ------------------------------------------------------------------------
+// Op-level kernels
+// ------------------------------------------------------------------------
+
+// One wave per query row; lanes stride over keys.
+__global__ __launch_bounds__(256) void qk_requant_rowmax_kernel(
+    const int8_t *__restrict__ q, const int8_t *__restrict__ k, const uint8_t *__restrict__ mask,
+    int16_t *__restrict__ qk, int16_t *__restrict__ rmp1, int64_t rows, int64_t tq, int64_t tk,
+    int64_t dim, uint32_t m, uint32_t s) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t bh = row / tq, i = row % tq;
+  const int8_t *qr = q + row * dim;
+  const int8_t *kb = k + bh * tk * dim;
+  int16_t *o = qk + row * tk;
+  int32_t mx = -32768;
+  for (int64_t j = lane; j < tk; j += 64) {
+    if (mask && mask[i * tk + j]) {
+      o[j] = -32768;
+      continue;
+    }
+    const int8_t *kr = kb + j * dim;
+    int32_t acc = 0;
+    for (int64_t d = 0; d < dim; ++d) acc += (int32_t)qr[d] * (int32_t)kr[d];
+    const int32_t h = qk_requant16(acc, m, s);
+    o[j] = (int16_t)h;
+    mx = max(mx, h);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  if (lane == 0) rmp1[row] = (int16_t)(uint16_t)((uint32_t)(uint16_t)(int16_t)mx + 1u);
+}
+
+__global__ __launch_bounds__(256) void shift_exp_kernel(const int16_t *__restrict__ qk,
+                                                        const int16_t *__restrict__ rmp1,
+                                                        const uint8_t *__restrict__ mask,
+                                                        uint8_t *__restrict__ p,
+                                                        int32_t *__restrict__ row_sum,
+                                                        int64_t rows, int64_t tq, int64_t tk,
+                                                        int32_t f) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t i = row % tq;
+  const int16_t xm = rmp1[row];
+  uint32_t sum = 0;
+  for (int64_t j = lane; j < tk; j += 64) {
+    uint32_t v = 0;
+    if (!(mask && mask[i * tk + j])) {
+      const int32_t xs = (int16_t)(uint16_t)((uint32_t)(uint16_t)qk[row * tk + j] - (uint32_t)(uint16_t)xm);
+      v = shift_exp_one(xs, f);
+    }
+    p[row * tk + j] = (uint8_t)v;
+    sum += v;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off);
+  if (lane == 0) row_sum[row] = (int32_t)sum;
+}
+
+// One block per query row; each wave owns a subset of the head dims.
+__global__ __launch_bounds__(256) void pv_norm_requant_kernel(
+    const uint8_t *__restrict__ p, const int8_t *__restrict__ v, const int32_t *__restrict__ rsum,
+    uint32_t av_m, uint32_t av_s, uint32_t off, int8_t *__restrict__ out, int64_t heads,
+    int64_t tq, int64_t tk, int64_t dim) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;  // (b*H + h)*Tq + i
+  const int64_t bh = row / tq, i = row % tq;
+  const int64_t b = bh / heads, h = bh % heads;
+  const uint8_t *pr = p + row * tk;
+  const int32_t inv = fisr(rsum[row], off);
+  for (int64_t d = wave; d < dim; d += 4) {
+    const int8_t *vr = v + (bh * dim + d) * tk;
+    uint32_t acc = 0;
+    for (int64_t j = lane; j < tk; j += 64) acc += (uint32_t)((int32_t)pr[j] * (int32_t)vr[j]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += (uint32_t)__shfl_xor((int)acc, o);
+    if (lane == 0) {
+      int32_t y = rshift((int32_t)(acc * (uint32_t)inv), off);
+      y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), off);
+      y = rshift((int32_t)((uint32_t)y * av_m), av_s);
+      out[(b * tq + i) * heads * dim + h * dim + d] = (int8_t)clampi(y, -127, 127);
+    }
+  }
+}
+
+// Shift-exp table for one frac_bits value: lut[i] = P(x_sub = -i) for
+// i in [0, 32767]. Every x_sub <= -32767 and every x_sub > 0 maps to 0, so an
+// index min((uint16)(rmp1 - qk), 32767) covers all int16 inputs.
+__global__ void shift_exp_lut_kernel(uint8_t *lut, int32_t f) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < IW_SEXP_LUT) lut[i] = (uint8_t)shift_exp_one(-i, f);
+}
+
+// ------------------------------------------------------------------------
+// Fused prefill attention (MFMA)
+// ------------------------------------------------------------------------
+//
+// Block: 4 waves x 32 query rows of one (batch, head); persistent over tiles.
+// Scores are computed transposed, S^T = K . Q^T, with MFMA 32x32x32: lane l
+// owns query l % 32 and, for register r, the key held in LDS row
+// (r/4)*8 + (l/32)*4 + r%4 of the 32-key sub-block. Keys are stored in LDS in
+// the order that puts key 16*(l/32) + r in that row, so each lane holds 16
+// consecutive keys of its query — exactly the A-operand layout of the P.V
+// MFMA, whose B operand is then one 16-byte read of V^T from LDS.
+
+constexpr int PF_KC = 64;  // keys per LDS stage
+
+__device__ __forceinline__ int key_row(int kk) {
+  // LDS row of key kk (0..31) inside a 32-key sub-block
+  const int g = kk >> 4, r = kk & 15;
+  return (r >> 2) * 8 + g * 4 + (r & 3);
+}
+
+template <int KS, bool HAS_MASK>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
+  constexpr int DP = KS * 32;           // padded head dim
+  constexpr int KLD = DP + 16;          // sK row stride
+  constexpr int VLD = PF_KC + 16;       // sVt row stride
+  __shared__ __attribute__((aligned(16))) uint8_t sLut[IW_SEXP_LUT];
+  __shared__ __attribute__((aligned(16))) int8_t sK[PF_KC * KLD];
+  __shared__ __attribute__((aligned(16))) int8_t sVt[DP * VLD];
+  __shared__ int32_t sInv[4][32];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, ql = lane & 31;
+
+  for (int i = tid; i < IW_SEXP_LUT / 16; i += 256)
+    reinterpret_cast<uint4 *>(sLut)[i] = reinterpret_cast<const uint4 *>(a.lut)[i];
+
+  const int qtiles = (a.Tq + 127) / 128;
+  const int64_t ntiles = (int64_t)qtiles * a.H * a.B;
+  const int nkc = (a.Tk + PF_KC - 1) / PF_KC;
+  const int D = a.D;
+
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int qt = (int)(tile % qtiles);
+    const int64_t bh = tile / qtiles;
+    const int h = (int)(bh % a.H);
+    const int64_t b = bh / a.H;
+    const int q = qt * 128 + wave * 32 + ql;  // this lane's query row
+    const int8_t *kbase = a.k + b * a.k_sb + (int64_t)h * D;
+    const int8_t *vbase = a.vt + (b * a.H + h) * (int64_t)D * a.vt_ld;
+
+    v4i qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = ks * 32 + g * 16;
+      if (q < a.Tq && d0 < D)
+        qf[ks] = *reinterpret_cast<const v4i *>(a.q + b * a.q_sb + (int64_t)q * a.q_st +
+                                                 (int64_t)h * D + d0);
+      else
+        qf[ks] = v4i{0, 0, 0, 0};
+    }
+
+    auto stage_k = [&](int kc) {
+      constexpr int CPK = DP / 16;  // 16-byte chunks per key row
+      for (int c = tid; c < PF_KC * CPK; c += 256) {
+        const int kk = c / CPK, part = c % CPK;
+        const int key = kc * PF_KC + kk;
+        uint4 val = make_uint4(0, 0, 0, 0);
+        if (key < a.Tk && part * 16 < D)
+          val = *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * a.k_st + part * 16);
+        const int row = (kk & 32) + key_row(kk & 31);
+        *reinterpret_cast<uint4 *>(&sK[row * KLD + part * 16]) = val;
+      }
+    };
+    auto scores = [&](int sub) {
+      v16i s;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = 0;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const v4i ka = *reinterpret_cast<const v4i *>(&sK[(sub * 32 + ql) * KLD + ks * 32 + g * 16]);
+        s = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka, qf[ks], s, 0, 0, 0);
+      }
+      return s;
+    };
+
+    // ---- pass 1: row max of the raw scores over unmasked keys ----
+    int32_t mx = INT32_MIN;
+    for (int kc = 0; kc < nkc; ++kc) {
+      stage_k(kc);
+      __syncthreads();
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const v16i s = scores(sub);
+        const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kbase0 + r;
+          bool ok = key < a.Tk;
+          if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
+          if (ok) mx = max(mx, s[r]);
+        }
+      }
+      __syncthreads();
+    }
+    mx = max(mx, __shfl_xor(mx, 32));
+    const int32_t rowmax = mx == INT32_MIN ? -32768 : qk_requant16(mx, a.qk_m, a.qk_s);
+    const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
+
+    // ---- pass 2: P = E(S - rmp1) and O = P . V ----
+    v16i o[KS];
+#pragma unroll
+    for (int t = 0; t < KS; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] = 0;
+    uint32_t psum = 0;
+    for (int kc = 0; kc < nkc; ++kc) {
+      stage_k(kc);
+      // V^T chunk: rows d, 64 keys each (4 chunks of 16 bytes)
+      for (int c = tid; c < DP * 4; c += 256) {
+        const int d = c >> 2, part = c & 3;
+        const int key0 = kc * PF_KC + part * 16;
+        uint4 val = make_uint4(0, 0, 0, 0);
+        if (d < D && key0 < a.vt_ld)
+          val = *reinterpret_cast<const uint4 *>(vbase + (int64_t)d * a.vt_ld + key0);
+        *reinterpret_cast<uint4 *>(&sVt[d * VLD + part * 16]) = val;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const v16i s = scores(sub);
+        const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
+        uint32_t pw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kbase0 + r;
+          bool ok = key < a.Tk;
+          if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
+          const int32_t h16 = qk_requant16(s[r], a.qk_m, a.qk_s);
+          const uint32_t idx = min((uint32_t)(uint16_t)(rmp1 - (uint32_t)h16), (uint32_t)(IW_SEXP_LUT - 1));
+          const uint32_t pv = ok ? (uint32_t)sLut[idx] : 0u;
+          pw[r >> 2] |= pv << (8 * (r & 3));
+        }
+        const uint32_t ones = 0x01010101u;
+        psum = __builtin_amdgcn_udot4(pw[0], ones, psum, false);
+        psum = __builtin_amdgcn_udot4(pw[1], ones, psum, false);
+        psum = __builtin_amdgcn_udot4(pw[2], ones, psum, false);
+        psum = __builtin_amdgcn_udot4(pw[3], ones, psum, false);
+        // P <= 127 except at x_sub == 0 after an int16 row-max wrap (P = 128).
+        // int8 MFMA is signed, so such tiles split P = lo + 64 * hi2.
+        const uint32_t hib = (pw[0] | pw[1] | pw[2] | pw[3]) & 0x80808080u;
+        const bool any_hi = __any(hib != 0u);
+        v4i pa, ph;
+        if (!any_hi) {
+          pa = v4i{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
+        } else {
+          pa = v4i{(int)(pw[0] & 0x7f7f7f7fu), (int)(pw[1] & 0x7f7f7f7fu),
+                   (int)(pw[2] & 0x7f7f7f7fu), (int)(pw[3] & 0x7f7f7f7fu)};
+          ph = v4i{(int)((pw[0] >> 1) & 0x40404040u), (int)((pw[1] >> 1) & 0x40404040u),
+                   (int)((pw[2] >> 1) & 0x40404040u), (int)((pw[3] >> 1) & 0x40404040u)};
+        }
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + sub * 32 + g * 16]);
+          o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, vb, o[t], 0, 0, 0);
+          if (any_hi) {
+            // 128 * hi = 64 * hi + 64 * hi
+            o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ph, vb, o[t], 0, 0, 0);
+            o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ph, vb, o[t], 0, 0, 0);
+          }
+        }
+      }
+      __syncthreads();
+    }
+    psum += (uint32_t)__shfl_xor((int)psum, 32);
+    if (g == 0) sInv[wave][ql] = fisr((int32_t)psum, a.rsqrt_off);
+    __syncthreads();
+
+    // ---- epilogue: lane owns head dim t*32 + l%32 for 16 query rows ----
+#pragma unroll
+    for (int t = 0; t < KS; ++t) {
+      const int d = t * 32 + ql;
+      if (d >= D) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = (r >> 2) * 8 + g * 4 + (r & 3);
+        const int qq = qt * 128 + wave * 32 + qr;
+        if (qq >= a.Tq) continue;
+        const int32_t inv = sInv[wave][qr];
+        int32_t y = rshift((int32_t)((uint32_t)o[t][r] * (uint32_t)inv), a.rsqrt_off);
+        y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+        y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+        a.out[b * a.o_sb + (int64_t)qq * a.o_st + (int64_t)h * D + d] = (int8_t)clampi(y, -127, 127);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------------
+// Decode attention: one block per (batch, head, query row)
+// ------------------------------------------------------------------------
+constexpr int DEC_MAX_TK = 4096;
+
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+  __shared__ int32_t sS[DEC_MAX_TK];
+  __shared__ __attribute__((aligned(16))) uint8_t sP[DEC_MAX_TK];
+  __shared__ int32_t sRed[8];
+  __shared__ uint32_t sSum[8];
+  __shared__ uint32_t sHi;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qi = blockIdx.y;
+  const int64_t bh = blockIdx.x;
+  const int h = (int)(bh % a.H);
+  const int64_t b = bh / a.H;
+  const int D = a.D;
+  const int nq = D >> 4;  // 16-byte chunks per row (D % 16 == 0, D <= 128)
+  if (tid == 0) sHi = 0;
+
+  uint4 qv[8];
+  const int8_t *qr = a.q + b * a.q_sb + (int64_t)qi * a.q_st + (int64_t)h * D;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) qv[c] = c < nq ? reinterpret_cast<const uint4 *>(qr)[c] : make_uint4(0, 0, 0, 0);
+  const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh;
+
+  // phase 1: raw scores and their max over unmasked keys
+  int32_t mx = INT32_MIN;
+  for (int j = tid; j < a.Tk; j += 256) {
+    const uint4 *kr = reinterpret_cast<const uint4 *>(kb + (int64_t)j * a.k_st);
+    int32_t acc = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (c < nq) {
+        const uint4 kv = kr[c];
+        acc = __builtin_amdgcn_sdot4((int)qv[c].x, (int)kv.x, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)qv[c].y, (int)kv.y, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)qv[c].z, (int)kv.z, acc, false);
+        acc = __builtin_amdgcn_sdot4((int)qv[c].w, (int)kv.w, acc, false);
+      }
+    }
+    sS[j] = acc;
+    const bool ok = !(a.mask && a.mask[(int64_t)qi * a.Tk + j]);
+    if (ok) mx = max(mx, acc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  if (lane == 0) sRed[wave] = mx;
+  __syncthreads();
+  mx = max(max(sRed[0], sRed[1]), max(sRed[2], sRed[3]));
+  const int32_t rowmax = mx == INT32_MIN ? -32768 : qk_requant16(mx, a.qk_m, a.qk_s);
+  const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
+
+  // phase 2: P and its sum
+  uint32_t psum = 0, hi = 0;
+  for (int j = tid; j < a.Tk; j += 256) {
+    uint32_t p = 0;
+    if (!(a.mask && a.mask[(int64_t)qi * a.Tk + j])) {
+      const int32_t h16 = qk_requant16(sS[j], a.qk_m, a.qk_s);
+      // x_sub = qk - rmp1 modulo 2^16
+      p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)h16 - rmp1), a.frac_bits);
+    }
+    sP[j] = (uint8_t)p;
+    psum += p;
+    hi |= p;
+  }
+  // zero the tail of the last 16-byte chunk
+  const int tk16 = (a.Tk + 15) & ~15;
+  for (int j = a.Tk + tid; j < tk16; j += 256) sP[j] = 0;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) psum += (uint32_t)__shfl_xor((int)psum, off);
+  if (lane == 0) sSum[wave] = psum;
+  if (hi & 0x80u) atomicOr(&sHi, 1u);
+  __syncthreads();
+  const int32_t total = (int32_t)(sSum[0] + sSum[1] + sSum[2] + sSum[3]);
+  const int32_t inv = fisr(total, a.rsqrt_off);
+  const bool any_hi = sHi != 0;
+
+  // phase 3: O[d] = sum_j P[j] V^T[d][j]; 256 / D threads per head dim
+  int tpd = 1;  // threads per head dim: largest power of two <= 256 / D
+  while (tpd * 2 * D <= 256) tpd *= 2;
+  const int d = tid / tpd, part = tid % tpd;
+  const int8_t *vr = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)(d < D ? d : 0) * a.v_sd;
+  uint32_t acc = 0;
+  const int nchunk = d < D ? (tk16 >> 4) : 0;
+  for (int c = part; c < nchunk; c += tpd) {
+    uint4 pv = reinterpret_cast<const uint4 *>(sP)[c];
+    uint4 vv = *reinterpret_cast<const uint4 *>(vr + c * 16);
+    // keys beyond Tk have P = 0
+    if (!any_hi) {
+      acc = (uint32_t)__builtin_amdgcn_sdot4((int)pv.x, (int)vv.x, (int)acc, false);
+      acc = (uint32_t)__builtin_amdgcn_sdot4((int)pv.y, (int)vv.y, (int)acc, false);
+      acc = (uint32_t)__builtin_amdgcn_sdot4((int)pv.z, (int)vv.z, (int)acc, false);
+      acc = (uint32_t)__builtin_amdgcn_sdot4((int)pv.w, (int)vv.w, (int)acc, false);
+    } else {
+      const uint32_t lo[4] = {pv.x & 0x7f7f7f7fu, pv.y & 0x7f7f7f7fu, pv.z & 0x7f7f7f7fu, pv.w & 0x7f7f7f7fu};
+      const uint32_t hb[4] = {(pv.x >> 7) & 0x01010101u, (pv.y >> 7) & 0x01010101u,
+                              (pv.z >> 7) & 0x01010101u, (pv.w >> 7) & 0x01010101u};
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+      int32_t hs = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc = (uint32_t)__builtin_amdgcn_sdot4((int)lo[e], (int)vw[e], (int)acc, false);
+        hs = __builtin_amdgcn_sdot4((int)hb[e], (int)vw[e], hs, false);
+      }
+      acc += (uint32_t)hs << 7;
+    }
+  }
+  for (int off = 1; off < tpd; off <<= 1) acc += (uint32_t)__shfl_xor((int)acc, off);
+  if (part == 0 && d < D) {
+    int32_t y = rshift((int32_t)(acc * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+    a.out[b * a.o_sb + (int64_t)qi * a.o_st + (int64_t)h * D + d] = (int8_t)clampi(y, -127, 127);
+  }
+}
+
+}  // namespace
+
+int launch_qk_requant_rowmax(const int8_t *q, const int8_t *k, const uint8_t *mask, int16_t *qk,
+                             int16_t *rmp1, int64_t bh, int64_t tq, int64_t tk, int64_t dim,
+                             uint8_t m, int32_t shift, hipStream_t s) {
+  const int64_t rows = bh * tq;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(qk_requant_rowmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, q,
+                     k, mask, qk, rmp1, rows, tq, tk, dim, (uint32_t)m,
+                     (uint32_t)(shift > 0 ? shift : 0));
+  return check_launch("qk_requant_rowmax_kernel");
+}
+
+int launch_shift_exp(const int16_t *qk, const int16_t *rmp1, const uint8_t *mask, uint8_t *p,
+                     int32_t *row_sum, int64_t bh, int64_t tq, int64_t tk, int32_t f,
+                     hipStream_t s) {
+  const int64_t rows = bh * tq;
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(shift_exp_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, qk, rmp1,
+                     mask, p, row_sum, rows, tq, tk, f);
+  return check_launch("shift_exp_kernel");
+}
+
+int launch_pv_norm_requant(const uint8_t *p, const int8_t *v, const int32_t *row_sum, uint8_t av_m,
+                           int8_t av_s, uint32_t off, int8_t *out, int64_t batch, int64_t heads,
+                           int64_t tq, int64_t tk, int64_t dim, hipStream_t s) {
+  const int64_t rows = batch * heads * tq;
+  if (rows == 0) return 0;
+  const int32_t as = av_s;
+  hipLaunchKernelGGL(pv_norm_requant_kernel, dim3((unsigned)rows), dim3(256), 0, s, p, v, row_sum,
+                     (uint32_t)av_m, (uint32_t)(as < 0 ? 0 : (as > 32 ? 32 : as)), off, out, heads,
+                     tq, tk, dim);
+  return check_launch("pv_norm_requant_kernel");
+}
+
+int launch_shift_exp_lut(uint8_t *lut, int32_t f, hipStream_t s) {
+  hipLaunchKernelGGL(shift_exp_lut_kernel, dim3(IW_SEXP_LUT / 256), dim3(256), 0, s, lut, f);
+  return check_launch("shift_exp_lut_kernel");
+}
+
+int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s) {
+  const int64_t tiles = (int64_t)((a.Tq + 127) / 128) * a.H * a.B;
+  if (tiles == 0) return 0;
+  const unsigned grid = (unsigned)(tiles < max_blocks ? tiles : max_blocks);
+  const int ks = (a.D + 31) / 32;
+#define IW_PF(KS_)                                                                          \
+  if (a.mask)                                                                               \
+    hipLaunchKernelGGL((attn_prefill_kernel<KS_, true>), dim3(grid), dim3(256), 0, s, a);   \
+  else                                                                                      \
+    hipLaunchKernelGGL((attn_prefill_kernel<KS_, false>), dim3(grid), dim3(256), 0, s, a);
+  switch (ks) {
+    case 1: IW_PF(1) break;
+    case 2: IW_PF(2) break;
+    case 3: IW_PF(3) break;
+    case 4: IW_PF(4) break;
+    default: return fail("fused attention supports head_dim <= 128");
+  }
+#undef IW_PF
+  return check_launch("attn_prefill_kernel");
+}
+
+int launch_attn_decode(const AttnArgs &a, hipStream_t s) {
+  if ((int64_t)a.B * a.H * a.Tq == 0) return 0;
+  if (a.Tk > DEC_MAX_TK) return fail("decode attention supports at most 4096 keys");
+  hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)(a.B * a.H), (unsigned)a.Tq), dim3(256), 0,
+                     s, a);
+  return check_launch("attn_decode_kernel");
+}
+
+}  // namespace iw

@@ -1,0 +1,129 @@
+// Shared device helpers for the I-Whisper integer kernels on gfx950.
+//
+// The fixed-point primitives restate i_whisper/kernels/csrc/common/fixedpoint.h:35-102
+// bit for bit: mulh is the high word of the signed-by-unsigned 64-bit product,
+// rshift rounds half away from zero with a modulo-2^32 add, shift 0 is the
+// identity and shift >= 32 gives 0.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace iw {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int32_t mulh(int32_t x, uint32_t m) {
+  return (int32_t)(((int64_t)x * (int64_t)(uint64_t)m) >> 32);
+}
+
+__device__ __forceinline__ int32_t rshift(int32_t x, uint32_t s) {
+  if (s == 0) return x;
+  if (s >= 32) return 0;
+  uint32_t bias = (1u << (s - 1)) - ((uint32_t)x >> 31);
+  return (int32_t)((uint32_t)x + bias) >> s;
+}
+
+// rshift for 1 <= s <= 31 known on entry (no special cases).
+__device__ __forceinline__ int32_t rshift_pos(int32_t x, uint32_t s) {
+  uint32_t bias = (1u << (s - 1)) + (uint32_t)(x >> 31);
+  return (int32_t)((uint32_t)x + bias) >> s;
+}
+
+__device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
+  return min(max(v, lo), hi);
+}
+
+__device__ __forceinline__ uint32_t clamp_shift_0_32(int32_t s) {
+  return (uint32_t)min(max(s, 0), 32);
+}
+
+// Integer GeLU on one int8 value (gelu/gelu_scalar.cpp:29-180).
+__device__ __forceinline__ int8_t gelu_one(int32_t x, const uint8_t *lut, uint32_t luti_m,
+                                           int32_t luti_s, uint32_t luto_m, int32_t luto_s) {
+  int32_t idx = rshift(x * (int32_t)luti_m, clamp_shift_0_32(luti_s)) + 8;
+  idx = clampi(idx, 0, 15);
+  int32_t v = x * (int32_t)lut[idx];
+  v = (int32_t)((uint32_t)v * luto_m);
+  v = rshift(v, clamp_shift_0_32(luto_s));
+  return (int8_t)clampi(v, -127, 127);
+}
+
+// Integer fast inverse square root, two Newton steps
+// (layernorm/layernorm_scalar.cpp:309-438).
+__device__ __forceinline__ int32_t bitlen(int32_t v) { return v == 0 ? 0 : 32 - __clz(v); }
+
+__device__ inline int32_t fisr(int32_t x, uint32_t off) {
+  int32_t i;
+  if (x == 0) {
+    i = 0;
+  } else {
+    int32_t e = bitlen(x) - 1;
+    uint32_t ux = (uint32_t)x;
+    uint32_t sig = e <= 23 ? (ux << (23 - e)) : (ux >> (e - 23));
+    i = (int32_t)(((uint32_t)(e + 127) << 23) | (sig & 0x007FFFFFu));
+  }
+  i = (int32_t)(0x5f3759dfu - (uint32_t)(i >> 1));
+  uint32_t raw = (uint32_t)i + (off << 23);
+  int32_t e = (int32_t)((raw >> 23) & 0xFFu) - 127;
+  uint64_t sig = (uint64_t)((1u << 23) | (raw & 0x007FFFFFu));
+  int32_t y;
+  if (e < 0) {
+    y = 0;
+  } else {
+    uint64_t v = e >= 23 ? (sig << (e - 23)) : (sig >> (23 - e));
+    y = (int32_t)(uint32_t)v;
+  }
+  uint32_t three = 3u << off;
+  for (int it = 0; it < 2; ++it) {
+    int32_t xy = (int32_t)((uint32_t)x * (uint32_t)y);
+    int32_t xs = rshift(xy, off);
+    uint32_t t = (uint32_t)xs * (uint32_t)y;
+    int32_t prod = (int32_t)((uint32_t)y * (three - t));
+    y = rshift(prod, off + 1);
+  }
+  return y;
+}
+
+// One lane of the shift-exponential (attention/attention_scalar.cpp:449-554),
+// int16 arithmetic modulo 2^16. Used to fill the per-launch lookup table.
+__device__ inline uint32_t shift_exp_one(int32_t x_sub16, int32_t f) {
+  int16_t xs = (int16_t)x_sub16;
+  if (xs > 0) return 0;
+  int16_t half = (int16_t)(xs >> 1);
+  int16_t six = (int16_t)(xs >> 4);
+  int16_t fix = (int16_t)(uint16_t)((uint16_t)(uint16_t)(xs + half) - (uint16_t)six);
+  int16_t xi = (int16_t)(fix >> f);
+  int16_t ip = (int16_t)(uint16_t)(uint32_t)((int32_t)xi * (1 << f));
+  int16_t frac = (int16_t)(uint16_t)(uint32_t)((int32_t)fix - (int32_t)ip);
+  int16_t num = (int16_t)(uint16_t)(uint32_t)((1 << f) + (int32_t)(frac >> 1));
+  int32_t e;
+  if (xi > 0) {
+    e = 0;
+  } else {
+    int32_t sh = -(int32_t)xi;
+    e = sh >= 16 ? 0 : (int32_t)(int16_t)(num >> sh);
+  }
+  int32_t o = f > 7 ? (e >> (f - 7)) : e;
+  return (uint32_t)(uint8_t)o;
+}
+
+}  // namespace iw
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing for the C ABI: every entry point returns 0 on
+// success or a negative code, and leaves a message for iw_last_error().
+// ---------------------------------------------------------------------------
+namespace iw {
+void set_error(const std::string &msg);
+int fail(const std::string &msg);  // sets the message, returns IW_EINVAL
+int check_launch(const char *what);
+}  // namespace iw
+
+#define IW_REQUIRE(cond, msg) \
+  do {                        \
+    if (!(cond)) return ::iw::fail(msg); \
+  } while (0)

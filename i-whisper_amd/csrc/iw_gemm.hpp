@@ -1,0 +1,65 @@
+// Argument block for the int8 MFMA GEMM (see iw_gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace iw {
+
+enum GemmEpi : int {
+  EPI_L8 = 0,      // Linear8 requant (per-channel mult/shift), optional GeLU
+  EPI_L32 = 1,     // Linear32: mulh << shift -> int32
+  EPI_L32RES = 2,  // Linear32 then residual15 -> int16
+  EPI_S8 = 3,      // per-tensor requant with shift clamped at 0 (classifier, conv),
+                   // optional GeLU, optional positional add_requant15 -> int16
+};
+
+enum GemmOut : int { OUT_ROW = 0, OUT_NCT = 1 };
+
+struct GemmArgs {
+  // A operand
+  const int8_t *a = nullptr;
+  int64_t lda = 0;
+  // implicit-GEMM conv geometry (A = conv input)
+  int64_t conv_tin = 0, conv_cin = 0, conv_stride = 1, conv_pad = 0, conv_tout = 1, conv_ksize = 1;
+  // B operand [N][K]
+  const int8_t *b = nullptr;
+  int64_t ldb = 0;
+  int64_t M = 0, N = 0, K = 0;
+  int epi = EPI_L8;
+  // epilogue parameters
+  const int32_t *bias = nullptr;
+  const int8_t *wz = nullptr;
+  const uint32_t *mult = nullptr;
+  const int8_t *shift = nullptr;
+  int mult_pc = 1;  // multiplier/shift per output channel (else one value)
+  uint32_t scalar_mult = 0;  // used when mult == nullptr
+  int8_t scalar_shift = 0;   // used when shift == nullptr
+  // fused GeLU (lut != nullptr enables it)
+  const uint8_t *lut = nullptr;
+  const uint8_t *luti_m = nullptr;
+  const int8_t *luti_s = nullptr;
+  const uint8_t *luto_m = nullptr;
+  const int8_t *luto_s = nullptr;
+  int luti_pc = 0, luto_pc = 0;
+  // fused residual15
+  const int16_t *res = nullptr;
+  int64_t ldres = 0;
+  uint32_t res_mult = 0;
+  // fused positional add_requant15 (pe != nullptr enables it; pe is [pe_T][N])
+  const int8_t *pe = nullptr;
+  const uint16_t *pe_mult = nullptr;
+  const int8_t *pe_shift = nullptr;
+  int pe_mpc = 0, pe_spc = 0;
+  int64_t pe_T = 1;
+  // output
+  void *out = nullptr;
+  int64_t ldc = 0;
+  int64_t out_T = 1;  // OUT_NCT: rows are (b, t) with t in [0, out_T)
+};
+
+int gemm_dense(const GemmArgs &g, hipStream_t s);
+int gemm_conv(const GemmArgs &g, bool channels_last, hipStream_t s);
+
+}  // namespace iw

@@ -1,0 +1,67 @@
+// Launch wrappers shared between the kernel files and the C ABI (iw_api.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#define IW_SEXP_LUT 32768  // shift-exp table entries (one byte each)
+
+namespace iw {
+
+// Fused attention arguments. Element (b, t, h, d) of a [B, T, H*D] operand
+// lives at base + b * sb + t * st + h * D + d. V is given transposed per
+// head: vt + b * v_sb + h * v_sh + d * v_sd + t (prefill: v_sh = D * vt_ld,
+// v_sd = vt_ld, v_sb = H * D * vt_ld).
+struct AttnArgs {
+  const int8_t *q = nullptr;
+  int64_t q_sb = 0, q_st = 0;
+  const int8_t *k = nullptr;
+  int64_t k_sb = 0, k_sh = 0, k_st = 0;  // decode: explicit per-head stride
+  const int8_t *vt = nullptr;
+  int64_t v_sb = 0, v_sh = 0, v_sd = 0, vt_ld = 0;
+  int8_t *out = nullptr;
+  int64_t o_sb = 0, o_st = 0;
+  const uint8_t *mask = nullptr;  // [Tq][Tk] bool bytes, or null
+  int32_t B = 0, H = 0, Tq = 0, Tk = 0, D = 0;
+  uint32_t qk_m = 0;   // uint8 multiplier
+  uint32_t qk_s = 0;   // shift clamped at 0
+  int32_t frac_bits = 7;
+  uint32_t av_m = 0;   // uint8 multiplier
+  uint32_t av_s = 0;   // shift clamped to [0, 32]
+  uint32_t rsqrt_off = 16;
+  const uint8_t *lut = nullptr;  // IW_SEXP_LUT entries for frac_bits
+};
+
+int layernorm_width_code(int64_t h);
+int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
+                       int8_t ln_s, uint32_t out_m, int8_t out_s, uint32_t rsqrt_off, int8_t *out,
+                       int64_t rows, int64_t hidden, hipStream_t s);
+int launch_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t off, hipStream_t s);
+int launch_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_m, const int8_t *luti_s,
+                const uint8_t *luto_m, const int8_t *luto_s, int8_t *out, int64_t numel,
+                int64_t channels, int luti_pc, int luto_pc, hipStream_t s);
+int launch_residual15(const int32_t *br, const int16_t *res, uint16_t m, int16_t *out, int64_t n,
+                      hipStream_t s);
+int launch_add_requant15(const int8_t *x, const int64_t *tokens, const int8_t *addend,
+                         const uint16_t *mult, const int8_t *shift, int16_t *out, int64_t batch,
+                         int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s);
+int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, int64_t m,
+                        int64_t t, hipStream_t s);
+int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
+                       hipStream_t s);
+
+int launch_qk_requant_rowmax(const int8_t *q, const int8_t *k, const uint8_t *mask, int16_t *qk,
+                             int16_t *rmp1, int64_t bh, int64_t tq, int64_t tk, int64_t dim,
+                             uint8_t m, int32_t shift, hipStream_t s);
+int launch_shift_exp(const int16_t *qk, const int16_t *rmp1, const uint8_t *mask, uint8_t *p,
+                     int32_t *row_sum, int64_t bh, int64_t tq, int64_t tk, int32_t f,
+                     hipStream_t s);
+int launch_pv_norm_requant(const uint8_t *p, const int8_t *v, const int32_t *row_sum, uint8_t av_m,
+                           int8_t av_s, uint32_t off, int8_t *out, int64_t batch, int64_t heads,
+                           int64_t tq, int64_t tk, int64_t dim, hipStream_t s);
+int launch_shift_exp_lut(uint8_t *lut, int32_t f, hipStream_t s);
+int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s);
+int launch_attn_decode(const AttnArgs &a, hipStream_t s);
+
+}  // namespace iw

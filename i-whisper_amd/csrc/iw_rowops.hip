@@ -1,0 +1,304 @@
+// Row-wise and element-wise integer kernels: LayerNorm32, FISR, GeLU,
+// residual15, add_requant15, token-embedding gather, log-mel quantization and
+// the greedy argmax. All are HBM-bound; each reads and writes its operands
+// once.
+#include "iw_common.hpp"
+#include "iw_kernels.hpp"
+
+namespace iw {
+
+namespace {
+
+// Division by the LayerNorm width as adds and floor shifts
+// (layernorm/layernorm_scalar.cpp:14-56), modulo 2^32.
+__device__ __forceinline__ int32_t norm_reduce(int32_t v, int code) {
+  switch (code) {
+    case 0: return (int32_t)((uint32_t)v + (uint32_t)(v >> 2) + (uint32_t)(v >> 3)) >> 9;
+    case 1: return v >> 9;
+    case 2: return (int32_t)((uint32_t)v + (uint32_t)(v >> 2) + (uint32_t)(v >> 3)) >> 10;
+    case 3: return v >> 10;
+    default: return (int32_t)((uint32_t)v + (uint32_t)(v >> 1)) >> 11;
+  }
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);
+  return v;
+}
+
+__device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o));
+  return v;
+}
+
+// LayerNorm32 (layernorm/layernorm_scalar.cpp:464-624), one wave per row.
+// The row lives in registers: lane l owns 4-element chunks l, l + 64, ...
+constexpr int LN_MAX_CHUNKS = 5;  // 1280 / 4 / 64
+
+__global__ __launch_bounds__(256) void layernorm32_kernel(
+    const int16_t *__restrict__ x, const int8_t *__restrict__ gamma,
+    const int32_t *__restrict__ beta, uint32_t ln_m, int32_t ln_s, uint32_t out_m,
+    int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int64_t rows, int hidden,
+    int code) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = hidden >> 2;
+  const int16_t *xr = x + row * hidden;
+  int32_t v[LN_MAX_CHUNKS][4];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch < nch) {
+      const uint2 w = *reinterpret_cast<const uint2 *>(xr + ch * 4);
+      v[c][0] = (int16_t)(w.x & 0xffff);
+      v[c][1] = (int16_t)(w.x >> 16);
+      v[c][2] = (int16_t)(w.y & 0xffff);
+      v[c][3] = (int16_t)(w.y >> 16);
+      sum += (uint32_t)(v[c][0] + v[c][1] + v[c][2] + v[c][3]);
+    } else {
+      v[c][0] = v[c][1] = v[c][2] = v[c][3] = 0;
+    }
+  }
+  const int32_t mean = norm_reduce((int32_t)wave_sum_u32(sum), code);
+  int32_t maxsq = 0;
+#pragma unroll
+  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+    if (lane + 64 * c < nch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t d = v[c][e] - mean;
+        maxsq = max(maxsq, (int32_t)((uint32_t)d * (uint32_t)d));
+      }
+    }
+  }
+  maxsq = wave_max_i32(maxsq);
+  int32_t rs = bitlen(maxsq) - 16;
+  rs = rs < 0 ? 0 : rs;
+  rs = (rs + 1) & ~1;
+  uint32_t vs = 0;
+#pragma unroll
+  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+    if (lane + 64 * c < nch) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t d = v[c][e] - mean;
+        vs += (uint32_t)rshift((int32_t)((uint32_t)d * (uint32_t)d), (uint32_t)rs);
+      }
+    }
+  }
+  const int32_t var = norm_reduce((int32_t)wave_sum_u32(vs), code);
+  const int32_t inv = fisr(var, rsqrt_off);
+  const uint32_t nshift = (uint32_t)(ln_s + (rs >> 1));
+  int8_t *orow = out + row * hidden;
+#pragma unroll
+  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch < nch) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int col = ch * 4 + e;
+        const int32_t d = v[c][e] - mean;
+        uint32_t t = (uint32_t)d * (uint32_t)inv * ln_m;
+        int32_t y = clampi(rshift((int32_t)t, nshift), -16383, 16383);
+        uint32_t a = (uint32_t)y * (uint32_t)(int32_t)gamma[col];
+        if (beta) a += (uint32_t)beta[col];
+        int32_t o = clampi(rshift(mulh((int32_t)a, out_m), (uint32_t)out_s), -127, 127);
+        packed |= ((uint32_t)(uint8_t)(int8_t)o) << (8 * e);
+      }
+      *reinterpret_cast<uint32_t *>(orow + ch * 4) = packed;
+    }
+  }
+}
+
+__global__ void rsqrt_kernel(const int32_t *x, int32_t *out, int64_t n, uint32_t off) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = fisr(x[i], off);
+}
+
+__global__ void gelu_kernel(const int8_t *__restrict__ x, const uint8_t *__restrict__ lut,
+                            const uint8_t *luti_m, const int8_t *luti_s, const uint8_t *luto_m,
+                            const int8_t *luto_s, int8_t *__restrict__ out, int64_t numel,
+                            int64_t channels, int luti_pc, int luto_pc) {
+  __shared__ uint8_t sl[16];
+  if (threadIdx.x < 16) sl[threadIdx.x] = lut[threadIdx.x];
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < numel; i += stride) {
+    const int64_t c = i % channels;
+    const int64_t a = luti_pc ? c : 0, b = luto_pc ? c : 0;
+    out[i] = gelu_one(x[i], sl, luti_m[a], luti_s[a], luto_m[b], luto_s[b]);
+  }
+}
+
+__global__ void residual15_kernel(const int32_t *__restrict__ br, const int16_t *__restrict__ res,
+                                  uint32_t m, int16_t *__restrict__ out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    uint32_t v = (uint32_t)br[i] + (uint32_t)((int32_t)res[i] * (int32_t)m);
+    out[i] = (int16_t)clampi(rshift_pos((int32_t)v, 15), -16383, 16383);
+  }
+}
+
+// add_requant15 (add_requant15/add_requant15_scalar.cpp:29-81). When tokens is
+// set, the int8 input row is gathered from the token embedding table first
+// (TextDecoder_int input, model_int.py:1411-1439).
+__global__ void add_requant15_kernel(const int8_t *__restrict__ x, const int64_t *__restrict__ tokens,
+                                     const int8_t *__restrict__ addend,
+                                     const uint16_t *__restrict__ mult,
+                                     const int8_t *__restrict__ shift, int16_t *__restrict__ out,
+                                     int64_t positions, int64_t channels, int64_t total, int mpc,
+                                     int spc) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % channels;
+    const int64_t bt = i / channels;
+    const int64_t t = bt % positions;
+    const int32_t xv = tokens ? (int32_t)x[tokens[bt] * channels + c] : (int32_t)x[i];
+    const int32_t v = xv + (int32_t)addend[t * channels + c];
+    const int32_t p = (int32_t)((uint32_t)v * (uint32_t)mult[mpc ? c : 0]);
+    const int32_t s = shift[spc ? c : 0];
+    out[i] = (int16_t)clampi(rshift(p, (uint32_t)(s < 0 ? 0 : s)), -16383, 16383);
+  }
+}
+
+// Encoder input quantization round(mel * alpha) clamped to +-127
+// (model_int.py:1265-1267; round half to even as torch.round), written
+// channels-last [B][T][n_mels] for the implicit-GEMM conv.
+__global__ void quantize_mel_kernel(const float *__restrict__ mel, float alpha,
+                                    int8_t *__restrict__ out, int64_t nb, int64_t nm, int64_t nt) {
+  const int64_t total = nb * nm * nt;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    // i indexes the output [b][t][m]
+    const int64_t m = i % nm;
+    const int64_t bt = i / nm;
+    const int64_t t = bt % nt, b = bt / nt;
+    const float v = __fmul_rn(mel[(b * nm + m) * nt + t], alpha);
+    float r = rintf(v);
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    out[i] = (int8_t)(int)r;
+  }
+}
+
+// First index of the row maximum (torch.argmax tie rule) over int8 logits.
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const int8_t *__restrict__ x,
+                                                          int64_t cols, int64_t ld,
+                                                          int64_t *__restrict__ out) {
+  const int64_t row = blockIdx.x;
+  const int8_t *xr = x + row * ld;
+  int32_t best = -1000;
+  int64_t bi = 0;
+  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+    const int32_t v = xr[c];
+    if (v > best) {
+      best = v;
+      bi = c;
+    }
+  }
+  __shared__ int32_t sv[256];
+  __shared__ int64_t si[256];
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      const int32_t ov = sv[threadIdx.x + s];
+      const int64_t oi = si[threadIdx.x + s];
+      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[row] = si[0];
+}
+
+int grid_for(int64_t n, int threads) {
+  int64_t b = (n + threads - 1) / threads;
+  if (b > 65536) b = 65536;
+  return (int)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+int layernorm_width_code(int64_t h) {
+  switch (h) {
+    case 384: return 0;
+    case 512: return 1;
+    case 768: return 2;
+    case 1024: return 3;
+    case 1280: return 4;
+    default: return -1;
+  }
+}
+
+int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
+                       int8_t ln_s, uint32_t out_m, int8_t out_s, uint32_t rsqrt_off, int8_t *out,
+                       int64_t rows, int64_t hidden, hipStream_t s) {
+  const int code = layernorm_width_code(hidden);
+  if (code < 0) return fail("unsupported LayerNorm hidden size: " + std::to_string(hidden));
+  if (rows == 0) return 0;
+  const int64_t blocks = (rows + 3) / 4;
+  hipLaunchKernelGGL(layernorm32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, gamma, beta,
+                     (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, rows,
+                     (int)hidden, code);
+  return check_launch("layernorm32_kernel");
+}
+
+int launch_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t off, hipStream_t s) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(rsqrt_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, out, n,
+                     off);
+  return check_launch("rsqrt_kernel");
+}
+
+int launch_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_m, const int8_t *luti_s,
+                const uint8_t *luto_m, const int8_t *luto_s, int8_t *out, int64_t numel,
+                int64_t channels, int luti_pc, int luto_pc, hipStream_t s) {
+  if (numel == 0) return 0;
+  hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(numel, 256)), dim3(256), 0, s, x, lut, luti_m,
+                     luti_s, luto_m, luto_s, out, numel, channels, luti_pc, luto_pc);
+  return check_launch("gelu_kernel");
+}
+
+int launch_residual15(const int32_t *br, const int16_t *res, uint16_t m, int16_t *out, int64_t n,
+                      hipStream_t s) {
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(residual15_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, br, res,
+                     (uint32_t)m, out, n);
+  return check_launch("residual15_kernel");
+}
+
+int launch_add_requant15(const int8_t *x, const int64_t *tokens, const int8_t *addend,
+                         const uint16_t *mult, const int8_t *shift, int16_t *out, int64_t batch,
+                         int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s) {
+  const int64_t total = batch * positions * channels;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(add_requant15_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, x, tokens,
+                     addend, mult, shift, out, positions, channels, total, mpc, spc);
+  return check_launch("add_requant15_kernel");
+}
+
+int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, int64_t m,
+                        int64_t t, hipStream_t s) {
+  const int64_t total = b * m * t;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(quantize_mel_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, mel, alpha,
+                     out, b, m, t);
+  return check_launch("quantize_mel_kernel");
+}
+
+int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
+                       hipStream_t s) {
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, cols, ld, out);
+  return check_launch("argmax_rows_kernel");
+}
+
+}  // namespace iw

@@ -1,0 +1,230 @@
+/*
+ * iwhisper_amd.h - C ABI of the MI355X (gfx950) kernels for I-Whisper's
+ * integer-only encoder/decoder path.
+ *
+ * Conventions
+ *   - Every tensor argument is a DEVICE pointer to contiguous memory in the
+ *     layout the reference uses for the same argument; the caller allocates
+ *     inputs and outputs (nothing is returned by allocation).
+ *   - Sizes are int64_t; scalar quantisation parameters are passed by value.
+ *   - `stream` is a hipStream_t (NULL selects the null stream). Calls are
+ *     asynchronous on that stream.
+ *   - Return value: IW_OK (0) or a negative code; iw_last_error() then holds a
+ *     message (per calling thread). No exception crosses the ABI.
+ *   - Integer semantics are bit-exact with the reference's scalar kernels,
+ *     including modulo-2^32 wrap of accumulators.
+ *
+ * Paths in the comments are relative to the reference repository root
+ * (vcsd-lab/I-Whisper); each drop-in entry point names the function of the
+ * reference's raw-pointer C++ API (csrc/<op>/<op>.h) and of its torch binding
+ * (csrc/<op>/<op>_torch.cpp, bound in csrc/pybind.cpp) that it replaces.
+ */
+#ifndef IWHISPER_AMD_H
+#define IWHISPER_AMD_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IW_OK 0
+#define IW_EINVAL (-1)  /* invalid argument (shape, size, parameter range) */
+#define IW_ELAUNCH (-2) /* HIP runtime error at launch */
+
+#define IW_ABI_VERSION 1
+#define IW_SHIFT_EXP_TABLE_BYTES 32768
+
+typedef void *iw_stream_t; /* hipStream_t */
+
+int iw_abi_version(void);
+const char *iw_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Drop-in replacements for the reference's per-op kernels.
+ * ------------------------------------------------------------------------- */
+
+/* Linear8: out[m,n] = clamp(requant(x.w + bias - wz*rowsum(x), mult[n], shift[n]), +-127).
+ * Replaces iwhisper::linear8_simd (i_whisper/kernels/csrc/linear8/linear8.h:26-38)
+ * behind _C.linear8_simd (linear8/linear8_torch.cpp:14-152, pybind.cpp:61-69).
+ * x [M,K] int8, weight [N,K] int8, bias [N] int32, weight_zero [N] int8,
+ * multiplier [N] uint32, shift [N] int8, out [M,N] int8. */
+int iw_linear8(const int8_t *x, const int8_t *weight, const int32_t *bias,
+               const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+               int8_t *out, int64_t M, int64_t K, int64_t N, bool has_bias, bool asymmetric,
+               iw_stream_t stream);
+
+/* Linear32: out[m,n] = (int32)(mulh(acc, mult[n]) << shift[n]) (0 for shifts outside [0,31]).
+ * Replaces iwhisper::linear32_simd (linear32/linear32.h:47-59) behind _C.linear32_simd
+ * (linear32/linear32_torch.cpp:10-150, pybind.cpp:92-100). out [M,N] int32. */
+int iw_linear32(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                int32_t *out, int64_t M, int64_t K, int64_t N, bool has_bias, bool asymmetric,
+                iw_stream_t stream);
+
+/* LayerNorm32 over rows of width hidden in {384, 512, 768, 1024, 1280}.
+ * Replaces iwhisper::layernorm32_simd (layernorm/layernorm.h:36-48) behind
+ * _C.layernorm32_simd (layernorm/layernorm_torch.cpp:200-305, pybind.cpp:141-150, which fixes
+ * rsqrt_offset = 13). x [rows,hidden] int16 -> out int8. */
+int iw_layernorm32(const int16_t *x, const int8_t *weight, const int32_t *bias,
+                   uint8_t ln_multiplier, int8_t ln_shift, uint32_t out_multiplier,
+                   int8_t out_shift, uint32_t rsqrt_offset, int8_t *out, int64_t rows,
+                   int64_t hidden, bool has_bias, iw_stream_t stream);
+
+/* Integer fast inverse square root, elementwise.
+ * Replaces iwhisper::layernorm32_rsqrt_scalar (layernorm/layernorm.h:30-34),
+ * _C.layernorm32_rsqrt_scalar (pybind.cpp:195-199). */
+int iw_layernorm32_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t offset,
+                         iw_stream_t stream);
+
+/* Integer GeLU (16-entry LUT). Parameter counts are 1 or channels.
+ * Replaces iwhisper::gelu_simd (gelu/gelu.h:21-32) behind _C.gelu_simd
+ * (gelu/gelu_torch.cpp:9-153, pybind.cpp:226-234). */
+int iw_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_multiplier,
+            const int8_t *luti_shift, const uint8_t *luto_multiplier, const int8_t *luto_shift,
+            int8_t *out, int64_t numel, int64_t channels, int64_t luti_count,
+            int64_t luto_count, iw_stream_t stream);
+
+/* out = clamp(Rshift(branch + residual*multiplier, 15), +-16383) int16.
+ * Replaces iwhisper::residual15_simd (residual15/residual15.h:15-20) behind
+ * _C.residual15_simd (residual15/residual15_torch.cpp:7-70, pybind.cpp:122-127). */
+int iw_residual15(const int32_t *branch, const int16_t *residual, uint16_t multiplier,
+                  int16_t *out, int64_t numel, iw_stream_t stream);
+
+/* out[b,t,c] = clamp(Rshift((x[b,t,c] + addend[t,c]) * m, max(s,0)), +-16383) int16.
+ * Replaces iwhisper::add_requant15_simd (add_requant15/add_requant15.h:17-28) behind
+ * _C.add_requant15_simd (add_requant15/add_requant15_torch.cpp:8-77, pybind.cpp:377-383). */
+int iw_add_requant15(const int8_t *x, const int8_t *addend, const uint16_t *multiplier,
+                     const int8_t *shift, int16_t *out, int64_t batch, int64_t positions,
+                     int64_t channels, int64_t multiplier_count, int64_t shift_count,
+                     iw_stream_t stream);
+
+/* int8 Conv1d (dilation 1, groups 1) + bias + per-tensor requant, [B,Cin,Tin] -> [B,Cout,Tout].
+ * weight is [Cout, Cin*kernel_size] with the kernel index fastest.
+ * Replaces iwhisper::conv1d_simd (conv1d/conv1d.h:71-85) behind _C.conv1d_simd
+ * (conv1d/conv1d_torch.cpp:243-340, pybind.cpp:357-366). */
+int iw_conv1d(const int8_t *x, const int8_t *weight, const int32_t *bias, uint32_t multiplier,
+              int8_t shift, int8_t *out, int64_t batch, int64_t in_channels,
+              int64_t input_length, int64_t out_channels, int64_t kernel_size, int64_t stride,
+              int64_t padding, bool has_bias, iw_stream_t stream);
+
+/* Logits before dequant: out = clamp(Rshift(mulh(x.E, m), max(s,0)), +-127) int8.
+ * Replaces iwhisper::classifier_simd (classifier/classifier.h:52-60) behind
+ * _C.classifier_simd (classifier/classifier_torch.cpp:145-212, pybind.cpp:407-414). */
+int iw_classifier(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift,
+                  int8_t *out, int64_t M, int64_t K, int64_t N, iw_stream_t stream);
+
+/* q [B,H,Tq,D], k [B,H,Tk,D] int8; mask [Tq,Tk] or NULL -> qk [B,H,Tq,Tk] int16,
+ * row_max_plus1 [B,H,Tq] int16. Replaces iwhisper::qk_requant_rowmax_simd
+ * (attention/attention.h:33-46) behind _C.qk_requant_rowmax_simd
+ * (attention/attention_torch.cpp:117-229, pybind.cpp:261-269). */
+int iw_qk_requant_rowmax(const int8_t *q, const int8_t *k, const bool *mask, int16_t *qk,
+                         int16_t *row_max_plus1, int64_t batch, int64_t heads, int64_t q_length,
+                         int64_t k_length, int64_t head_dim, uint8_t multiplier, int32_t shift,
+                         bool has_mask, iw_stream_t stream);
+
+/* qk [B,H,Tq,Tk] int16 -> p uint8 (same shape), row_sum [B,H,Tq] int32.
+ * frac_bits must be in [1, 13]. Replaces iwhisper::shift_exp_simd
+ * (attention/attention.h:71-82) behind _C.shift_exp_simd
+ * (attention/attention_torch.cpp:266-369, pybind.cpp:280-287). */
+int iw_shift_exp(const int16_t *qk, const int16_t *row_max_plus1, const bool *mask, uint8_t *p,
+                 int32_t *row_sum, int64_t batch, int64_t heads, int64_t q_length,
+                 int64_t k_length, int32_t frac_bits, bool has_mask, iw_stream_t stream);
+
+/* p [B,H,Tq,Tk] uint8, v [B,H,D,Tk] int8, row_sum [B,H,Tq] int32 (must be >= 0;
+ * the caller validates it, as the reference kernel throws) -> out [B,Tq,H*D] int8.
+ * rsqrt_offset must be in [0, 29]. Replaces iwhisper::pv_norm_requant_simd
+ * (attention/attention.h:151-164) behind _C.pv_norm_requant_simd
+ * (attention/attention_torch.cpp:523-669, pybind.cpp:314-322). */
+int iw_pv_norm_requant(const uint8_t *p, const int8_t *v, const int32_t *row_sum,
+                       uint8_t av_multiplier, int8_t av_shift, uint32_t rsqrt_offset,
+                       int8_t *out, int64_t batch, int64_t heads, int64_t q_length,
+                       int64_t k_length, int64_t head_dim, iw_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused entry points used by the MI355X layer API. Each is bit-identical to
+ * the chain of reference ops named in its comment; none has a single
+ * counterpart in the reference.
+ * ------------------------------------------------------------------------- */
+
+/* Linear8 followed by GELU_int on its int8 output (model_int.py:1103-1107,
+ * the MLP's first two modules). GeLU parameter counts are 1 or N. */
+int iw_linear8_gelu(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                    const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                    const uint8_t *lut, const uint8_t *luti_multiplier, const int8_t *luti_shift,
+                    const uint8_t *luto_multiplier, const int8_t *luto_shift, int64_t luti_count,
+                    int64_t luto_count, int8_t *out, int64_t M, int64_t K, int64_t N,
+                    bool has_bias, bool asymmetric, iw_stream_t stream);
+
+/* Linear32 followed by residual15 with the block input (model_int.py:1126-1169):
+ * out = residual15(linear32(x), residual, residual_multiplier), [M,N] int16.
+ * out may alias residual (each element is read before it is written). */
+int iw_linear32_residual15(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                           const int8_t *weight_zero, const uint32_t *multiplier,
+                           const int8_t *shift, const int16_t *residual,
+                           uint16_t residual_multiplier, int16_t *out, int64_t M, int64_t K,
+                           int64_t N, bool has_bias, bool asymmetric, iw_stream_t stream);
+
+/* Encoder input quantisation round(mel*alpha) clamped to +-127 (model_int.py:1265-1267,
+ * round half to even), mel [B,n_mels,T] float32 -> out [B,T,n_mels] int8 (channels-last). */
+int iw_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t batch, int64_t n_mels,
+                    int64_t frames, iw_stream_t stream);
+
+/* Channels-last Conv1d_int then GELU_int, optionally then the encoder's
+ * positional add_requant15 (model_int.py:1269-1296):
+ *   x [B,Tin,Cin] int8 (Cin % 16 == 0), weight_kc [Cout, kernel_size*Cin] (the
+ *   reference weight reordered to kernel-index-major), out [B,Tout,Cout].
+ * With pe == NULL the output is int8 (conv1 + gelu1); otherwise int16 =
+ * add_requant15(gelu(conv(x)), pe [Tout,Cout], pe_multiplier, pe_shift). */
+int iw_conv1d_cl(const int8_t *x, const int8_t *weight_kc, const int32_t *bias,
+                 uint32_t multiplier, int8_t shift, const uint8_t *lut,
+                 const uint8_t *luti_multiplier, const int8_t *luti_shift,
+                 const uint8_t *luto_multiplier, const int8_t *luto_shift, int64_t luti_count,
+                 int64_t luto_count, const int8_t *pe, const uint16_t *pe_multiplier,
+                 const int8_t *pe_shift, int64_t pe_multiplier_count, int64_t pe_shift_count,
+                 void *out, int64_t batch, int64_t in_channels, int64_t input_length,
+                 int64_t out_channels, int64_t kernel_size, int64_t stride, int64_t padding,
+                 bool has_bias, iw_stream_t stream);
+
+/* Decoder input: token-embedding gather then add_requant15 with the positional
+ * rows [offset, offset+T) (model_int.py:1411-1439). tokens [B,T] int64,
+ * table [vocab,C], pe [n_ctx,C], multiplier/shift scalars -> out [B,T,C] int16. */
+int iw_embed_add_requant15(const int64_t *tokens, const int8_t *table, const int8_t *pe,
+                           int64_t offset, const uint16_t *multiplier, const int8_t *shift,
+                           int16_t *out, int64_t batch, int64_t positions, int64_t channels,
+                           iw_stream_t stream);
+
+/* Fills the IW_SHIFT_EXP_TABLE_BYTES-entry table used by the fused attention:
+ * table[i] = shift_exp(x_sub = -i) for frac_bits in [1, 13]
+ * (attention/attention_scalar.cpp:449-554). */
+int iw_shift_exp_table(uint8_t *table, int32_t frac_bits, iw_stream_t stream);
+
+/* Fused MultiHeadAttention_int.qkv_attention (model_int.py:774-1040), i.e.
+ * qk_requant_rowmax -> shift_exp -> pv_norm_requant, without materialising the
+ * int16 scores or uint8 probabilities. q/k: element (b,t,h,d) at
+ * base + b*sb + t*st + h*head_dim + d; v is transposed per head:
+ * vt + b*v_sb + h*v_sh + d*v_sd + t (v_sd % 16 == 0 and at least round_up(k_length, 16)
+ * columns readable). out element (b,t,h,d) at out + b*o_sb + t*o_st + h*head_dim + d.
+ * head_dim % 16 == 0, head_dim <= 128. mask [Tq,Tk] bool or NULL.
+ * The prefill form uses int8 MFMA and needs the table from iw_shift_exp_table;
+ * the decode form (q_length <= 8, k_length <= 4096) takes table == NULL and also
+ * needs k_sh (per-head stride of k). */
+int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, int64_t k_sb,
+                 int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb, int64_t v_sh,
+                 int64_t v_sd, int8_t *out, int64_t o_sb, int64_t o_st, const bool *mask,
+                 int64_t batch, int64_t heads, int64_t q_length, int64_t k_length,
+                 int64_t head_dim, uint8_t qk_multiplier, int8_t qk_shift, int32_t frac_bits,
+                 uint8_t av_multiplier, int8_t av_shift, uint32_t rsqrt_offset,
+                 const uint8_t *table, bool decode, iw_stream_t stream);
+
+/* First index of the maximum of each row of int8 logits (greedy decoding,
+ * decoding.py:280-296 on the int8 logits, which dequantisation by a positive
+ * scale does not reorder). x [rows, ld], out [rows] int64. */
+int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
+                   iw_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IWHISPER_AMD_H */
