@@ -46,6 +46,8 @@ SIGNATURES = {
     "iw_attention": [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
                      _p, _i64, _i64, _i64, _i64, _i64, _u8, _i8, _i32, _u8, _i8, _u32, _p, _b, _p],
     "iw_argmax_rows": [_p, _i64, _i64, _i64, _p, _p],
+    "iw_transpose_heads": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "iw_copy_rows": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
 }
 
 _lock = threading.Lock()

@@ -470,6 +470,29 @@ int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, i
   return launch_attn_prefill(a, cus * 3, as_stream(stream));
 }
 
+int iw_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                       int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_offset,
+                       int64_t batch, int64_t positions, int64_t heads, int64_t head_dim,
+                       iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && positions >= 0 && heads > 0 && head_dim > 0 && t_offset >= 0,
+             "invalid transpose shape");
+  IW_REQUIRE(batch <= 65535, "batch too large for the transpose grid");
+  if (batch * positions == 0) return IW_OK;
+  IW_REQUIRE(src && dst, "null tensor pointer");
+  return launch_transpose_heads(src, src_sb, src_st, dst, dst_sb, dst_sh, dst_sd, t_offset, batch,
+                                positions, heads, head_dim, as_stream(stream));
+}
+
+int iw_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst, int64_t dst_sb,
+                 int64_t dst_st, int64_t t_offset, int64_t batch, int64_t positions,
+                 int64_t channels, iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && positions >= 0 && channels > 0 && t_offset >= 0, "invalid copy shape");
+  if (batch * positions == 0) return IW_OK;
+  IW_REQUIRE(src && dst, "null tensor pointer");
+  return launch_copy_rows(src, src_sb, src_st, dst, dst_sb, dst_st, t_offset, batch, positions,
+                          channels, as_stream(stream));
+}
+
 int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                    iw_stream_t stream) {
   IW_REQUIRE(rows >= 0 && cols > 0 && ld >= cols, "invalid argmax shape");

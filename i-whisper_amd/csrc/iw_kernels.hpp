@@ -50,6 +50,12 @@ int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, i
                         int64_t t, hipStream_t s);
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                        hipStream_t s);
+int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                           int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off,
+                           int64_t B, int64_t T, int64_t H, int64_t D, hipStream_t s);
+int launch_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                     int64_t dst_sb, int64_t dst_st, int64_t t_off, int64_t B, int64_t T,
+                     int64_t C, hipStream_t s);
 
 int launch_qk_requant_rowmax(const int8_t *q, const int8_t *k, const uint8_t *mask, int16_t *qk,
                              int16_t *rmp1, int64_t bh, int64_t tq, int64_t tk, int64_t dim,

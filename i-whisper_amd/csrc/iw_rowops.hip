@@ -219,6 +219,48 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const int8_t *__restri
   if (threadIdx.x == 0) out[row] = si[0];
 }
 
+// Per-head transpose of a [B, T, H*D] operand slice into V^T layout:
+// dst[b][h][d][t_off + t] = src[b*src_sb + t*src_st + h*D + d].
+// Tiles of 64 positions x 64 feature columns go through LDS so that both the
+// reads (along features) and the writes (along positions) are contiguous.
+__global__ __launch_bounds__(256) void transpose_heads_kernel(
+    const int8_t *__restrict__ src, int64_t src_sb, int64_t src_st, int8_t *__restrict__ dst,
+    int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off, int64_t T, int64_t H,
+    int64_t D) {
+  __shared__ int8_t tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  const int64_t c0 = (int64_t)blockIdx.y * 64;  // feature column h*D + d
+  const int64_t C = H * D;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t t = t0 + r, c = c0 + tx;
+    tile[r][tx] = (t < T && c < C) ? src[b * src_sb + t * src_st + c] : (int8_t)0;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t c = c0 + r, t = t0 + tx;
+    if (t < T && c < C) {
+      const int64_t h = c / D, d = c % D;
+      dst[b * dst_sb + h * dst_sh + d * dst_sd + t_off + t] = tile[tx][r];
+    }
+  }
+}
+
+// Copy rows of a [B, T, ld] operand slice (C features) into a [B, Tmax, C]
+// cache at positions [t_off, t_off + T).
+__global__ void copy_rows_kernel(const int8_t *__restrict__ src, int64_t src_sb, int64_t src_st,
+                                 int8_t *__restrict__ dst, int64_t dst_sb, int64_t dst_st,
+                                 int64_t t_off, int64_t B, int64_t T, int64_t C) {
+  const int64_t total = B * T * C;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % C, bt = i / C;
+    const int64_t t = bt % T, b = bt / T;
+    dst[b * dst_sb + (t_off + t) * dst_st + c] = src[b * src_sb + t * src_st + c];
+  }
+}
+
 int grid_for(int64_t n, int threads) {
   int64_t b = (n + threads - 1) / threads;
   if (b > 65536) b = 65536;
@@ -292,6 +334,26 @@ int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, i
   hipLaunchKernelGGL(quantize_mel_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, mel, alpha,
                      out, b, m, t);
   return check_launch("quantize_mel_kernel");
+}
+
+int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                           int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off,
+                           int64_t B, int64_t T, int64_t H, int64_t D, hipStream_t s) {
+  if (B * T * H * D == 0) return 0;
+  const dim3 grid((unsigned)((T + 63) / 64), (unsigned)((H * D + 63) / 64), (unsigned)B);
+  hipLaunchKernelGGL(transpose_heads_kernel, grid, dim3(256), 0, s, src, src_sb, src_st, dst,
+                     dst_sb, dst_sh, dst_sd, t_off, T, H, D);
+  return check_launch("transpose_heads_kernel");
+}
+
+int launch_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                     int64_t dst_sb, int64_t dst_st, int64_t t_off, int64_t B, int64_t T,
+                     int64_t C, hipStream_t s) {
+  const int64_t total = B * T * C;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, src, src_sb,
+                     src_st, dst, dst_sb, dst_st, t_off, B, T, C);
+  return check_launch("copy_rows_kernel");
 }
 
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,

@@ -1,0 +1,266 @@
+"""Batched encoder and greedy-decoder runners over a ``Whisper_int`` model.
+
+These drive the same gfx950 kernels as the layer API with the data layout
+chosen for the MI355X instead of the reference's per-call tensors:
+
+* Q/K/V (and cross-attention K/V) projections run as one GEMM over the
+  concatenated weights; the key projection has no bias, which equals a zero
+  bias in the concatenation.
+* The residual stream is one int16 buffer updated in place by the fused
+  Linear32 + residual15 kernels.
+* The decoder keeps preallocated KV caches: self-attention K as [B, n_ctx, C]
+  and V transposed per head [B, H, D, n_ctx]; cross-attention K/V are
+  projected once per utterance. This replaces the reference's hook-based
+  ``torch.cat`` cache (model_int.py:1587-1618) with identical values.
+* Greedy decoding feeds the last token each step (decoding.py:148-179,
+  684-712) and takes the first maximum of the int8 logits, a fixed number of
+  steps with no logit filters.
+"""
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+
+from . import _lib
+from .model_int import AudioEncoder_int, ResidualAttentionBlock_int, TextDecoder_int, Whisper_int
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class _FusedLinear:
+    """Several LinearBase layers sharing an input, as one [sum N, K] GEMM."""
+
+    def __init__(self, layers):
+        dev = layers[0].weight.device
+        self.K = layers[0].in_features
+        self.N = sum(l.out_features for l in layers)
+        self.weight = torch.cat([l.weight for l in layers]).contiguous()
+        biases = []
+        for l in layers:
+            biases.append(l.bias if l.bias is not None else
+                          torch.zeros(l.out_features, dtype=torch.int32, device=dev))
+        self.bias = torch.cat(biases).contiguous()
+        self.wz = torch.cat([l.wgt_zeros for l in layers]).contiguous()
+        self.mult = torch.cat([l.req_multiplier for l in layers]).contiguous()
+        self.shift = torch.cat([l.req_shiftmount for l in layers]).contiguous()
+
+    def linear8(self, x: torch.Tensor, M: int, out: torch.Tensor) -> torch.Tensor:
+        _lib.call("iw_linear8", x.data_ptr(), self.weight.data_ptr(), self.bias.data_ptr(),
+                  self.wz.data_ptr(), self.mult.data_ptr(), self.shift.data_ptr(), out.data_ptr(), M,
+                  self.K, self.N, True, True, _stream())
+        return out
+
+
+def _lin8(layer, x_ptr: int, M: int, out: torch.Tensor):
+    b, z = layer.bias, layer.wgt_zeros if layer.asym else None
+    _lib.call("iw_linear8", x_ptr, layer.weight.data_ptr(), _ptr(b), _ptr(z),
+              layer.req_multiplier.data_ptr(), layer.req_shiftmount.data_ptr(), out.data_ptr(), M,
+              layer.in_features, layer.out_features, b is not None, z is not None, _stream())
+    return out
+
+
+def _lin32_res(layer, x_ptr: int, M: int, res: torch.Tensor, res_mult: int):
+    b, z = layer.bias, layer.wgt_zeros if layer.asym else None
+    _lib.call("iw_linear32_residual15", x_ptr, layer.weight.data_ptr(), _ptr(b), _ptr(z),
+              layer.req_multiplier.data_ptr(), layer.req_shiftmount.data_ptr(), res.data_ptr(),
+              res_mult, res.data_ptr(), M, layer.in_features, layer.out_features, b is not None,
+              z is not None, _stream())
+
+
+def _ln(ln, x: torch.Tensor, rows: int, out: torch.Tensor):
+    s = ln._scalars()
+    _lib.call("iw_layernorm32", x.data_ptr(), ln.weight.data_ptr(), _ptr(ln.bias), s["lm"], s["ls"],
+              s["om"], s["os"], ln.offset, out.data_ptr(), rows, ln.normalized_shape[0],
+              ln.bias is not None, _stream())
+    return out
+
+
+def _mlp_gelu(block: ResidualAttentionBlock_int, x_ptr: int, M: int, out: torch.Tensor):
+    fc1, gelu = block.mlp[0], block.mlp[1]
+    lut, im, is_, om, os_, ci, co = gelu.gelu_ptrs()
+    _lib.call("iw_linear8_gelu", x_ptr, fc1.weight.data_ptr(), _ptr(fc1.bias),
+              _ptr(fc1.wgt_zeros), fc1.req_multiplier.data_ptr(), fc1.req_shiftmount.data_ptr(),
+              lut, im, is_, om, os_, ci, co, out.data_ptr(), M, fc1.in_features, fc1.out_features,
+              fc1.bias is not None, fc1.wgt_zeros is not None, _stream())
+    return out
+
+
+class EncoderRunner:
+    """AudioEncoder_int forward for a fixed batch with preallocated activations."""
+
+    def __init__(self, encoder: AudioEncoder_int, batch: int):
+        self.enc = encoder
+        self.B = batch
+        C, H, T = encoder.n_state, encoder.n_head, encoder.n_ctx
+        self.C, self.H, self.T, self.D = C, H, T, C // H
+        self.M = batch * T
+        dev = encoder.positional_embedding.device
+        self.qkv = [_FusedLinear([b.attn.query, b.attn.key, b.attn.value]) for b in encoder.blocks]
+        self.tp = (T + 15) // 16 * 16
+        self.h8 = torch.empty((self.M, C), dtype=torch.int8, device=dev)
+        self.qkv_buf = torch.empty((self.M, 3 * C), dtype=torch.int8, device=dev)
+        self.vt = torch.empty((batch, H, self.D, self.tp), dtype=torch.int8, device=dev)
+        self.wv = torch.empty((self.M, C), dtype=torch.int8, device=dev)
+        self.f8 = torch.empty((self.M, 4 * C), dtype=torch.int8, device=dev)
+        self.out = torch.empty((batch, T, C), dtype=torch.int8, device=dev)
+        self.tables = [b.attn.shift_exp_table() for b in encoder.blocks]
+
+    def block(self, i: int, x16: torch.Tensor):
+        blk = self.enc.blocks[i]
+        att = blk.attn
+        s = att._scalars()
+        sc = blk._scalars()
+        B, C, H, D, T, M = self.B, self.C, self.H, self.D, self.T, self.M
+        _ln(blk.attn_ln, x16, M, self.h8)
+        self.qkv[i].linear8(self.h8, M, self.qkv_buf)
+        q = self.qkv_buf.data_ptr()
+        _lib.call("iw_transpose_heads", q + 2 * C, T * 3 * C, 3 * C, self.vt.data_ptr(),
+                  H * D * self.tp, D * self.tp, self.tp, 0, B, T, H, D, _stream())
+        _lib.call("iw_attention", q, T * 3 * C, 3 * C, q + C, T * 3 * C, D, 3 * C,
+                  self.vt.data_ptr(), H * D * self.tp, D * self.tp, self.tp, self.wv.data_ptr(),
+                  T * C, C, None, B, H, T, T, D, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
+                  att.rsqrt_offset, self.tables[i].data_ptr(), False, _stream())
+        _lin32_res(att.out, self.wv.data_ptr(), M, x16, sc["a"])
+        _ln(blk.mlp_ln, x16, M, self.h8)
+        _mlp_gelu(blk, self.h8.data_ptr(), M, self.f8)
+        _lin32_res(blk.mlp[2], self.f8.data_ptr(), M, x16, sc["m"])
+
+    def __call__(self, mel: torch.Tensor) -> torch.Tensor:
+        x16 = self.enc.frontend(mel)
+        for i in range(len(self.enc.blocks)):
+            self.block(i, x16)
+        _ln(self.enc.ln_post, x16, self.M, self.out)
+        return self.out
+
+
+class DecoderRunner:
+    """Greedy TextDecoder_int steps over preallocated self/cross KV caches."""
+
+    def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int):
+        self.dec = decoder
+        self.B = batch
+        C, H = decoder.n_state, decoder.n_head
+        self.C, self.H, self.D = C, H, C // H
+        self.Tmax = (decoder.n_ctx + 15) // 16 * 16
+        self.Ta = n_audio_ctx
+        self.tpa = (n_audio_ctx + 15) // 16 * 16
+        dev = decoder.positional_embedding.device
+        L = decoder.n_layer
+        self.self_qkv = [_FusedLinear([b.attn.query, b.attn.key, b.attn.value]) for b in decoder.blocks]
+        self.cross_kv = [_FusedLinear([b.cross_attn.key, b.cross_attn.value]) for b in decoder.blocks]
+        self.k_self = [torch.empty((batch, self.Tmax, C), dtype=torch.int8, device=dev) for _ in range(L)]
+        self.vt_self = [torch.empty((batch, H, self.D, self.Tmax), dtype=torch.int8, device=dev)
+                        for _ in range(L)]
+        self.kv_cross = [torch.empty((batch * n_audio_ctx, 2 * C), dtype=torch.int8, device=dev)
+                         for _ in range(L)]
+        self.vt_cross = [torch.empty((batch, H, self.D, self.tpa), dtype=torch.int8, device=dev)
+                         for _ in range(L)]
+        self.offset = 0
+
+    def set_audio(self, xa: torch.Tensor):
+        """Project the cross-attention K/V of the encoder output once per utterance."""
+        xa = xa.contiguous()
+        B, Ta, C, H, D = self.B, self.Ta, self.C, self.H, self.D
+        for l in range(self.dec.n_layer):
+            kv = self.kv_cross[l]
+            self.cross_kv[l].linear8(xa, B * Ta, kv)
+            _lib.call("iw_transpose_heads", kv.data_ptr() + C, Ta * 2 * C, 2 * C,
+                      self.vt_cross[l].data_ptr(), H * D * self.tpa, D * self.tpa, self.tpa, 0, B, Ta,
+                      H, D, _stream())
+        self.offset = 0
+
+    def _attend(self, att, q_ptr, q_sb, q_st, k, k_sb, k_st, vt, tp, Tq, Tk, mask, out):
+        s = att._scalars()
+        H, D, C = self.H, self.D, self.C
+        _lib.call("iw_attention", q_ptr, q_sb, q_st, k.data_ptr(), k_sb, D, k_st, vt.data_ptr(),
+                  H * D * tp, D * tp, tp, out.data_ptr(), Tq * C, C, _ptr(mask), self.B, H, Tq, Tk,
+                  D, s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset, None, True,
+                  _stream())
+
+    def step(self, tokens: torch.Tensor, next_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Run the new ``tokens`` [B, T] (contiguous int64) and return the argmax of the
+        last position's int8 logits as int64 [B] (written into ``next_out`` if given)."""
+        dec = self.dec
+        B, C, H, D = self.B, self.C, self.H, self.D
+        T = tokens.shape[-1] if tokens.dim() == 2 else 1
+        off = self.offset
+        Tk = off + T
+        M = B * T
+        dev = tokens.device
+        x16 = dec.embed(tokens.view(B, T), off)
+        h8 = torch.empty((M, C), dtype=torch.int8, device=dev)
+        qkv = torch.empty((M, 3 * C), dtype=torch.int8, device=dev)
+        wv = torch.empty((M, C), dtype=torch.int8, device=dev)
+        qc = torch.empty((M, C), dtype=torch.int8, device=dev)
+        f8 = torch.empty((M, 4 * C), dtype=torch.int8, device=dev)
+        mask = dec.mask[off:off + T, :Tk].contiguous() if T > 1 else None
+        for l, blk in enumerate(dec.blocks):
+            sc = blk._scalars()
+            _ln(blk.attn_ln, x16, M, h8)
+            self.self_qkv[l].linear8(h8, M, qkv)
+            q = qkv.data_ptr()
+            _lib.call("iw_copy_rows", q + C, T * 3 * C, 3 * C, self.k_self[l].data_ptr(),
+                      self.Tmax * C, C, off, B, T, C, _stream())
+            _lib.call("iw_transpose_heads", q + 2 * C, T * 3 * C, 3 * C, self.vt_self[l].data_ptr(),
+                      H * D * self.Tmax, D * self.Tmax, self.Tmax, off, B, T, H, D, _stream())
+            self._attend(blk.attn, q, T * 3 * C, 3 * C, self.k_self[l], self.Tmax * C, C,
+                         self.vt_self[l], self.Tmax, T, Tk, mask, wv)
+            _lin32_res(blk.attn.out, wv.data_ptr(), M, x16, sc["a"])
+            _ln(blk.cross_attn_ln, x16, M, h8)
+            _lin8(blk.cross_attn.query, h8.data_ptr(), M, qc)
+            self._attend(blk.cross_attn, qc.data_ptr(), T * C, C, self.kv_cross[l], self.Ta * 2 * C,
+                         2 * C, self.vt_cross[l], self.tpa, T, self.Ta, None, wv)
+            _lin32_res(blk.cross_attn.out, wv.data_ptr(), M, x16, sc["c"])
+            _ln(blk.mlp_ln, x16, M, h8)
+            _mlp_gelu(blk, h8.data_ptr(), M, f8)
+            _lin32_res(blk.mlp[2], f8.data_ptr(), M, x16, sc["m"])
+        last = x16.view(B, T, C)[:, T - 1].contiguous()
+        hl = torch.empty((B, C), dtype=torch.int8, device=dev)
+        _ln(dec.ln, last, B, hl)
+        sc = dec.scalars()
+        logits = torch.empty((B, dec.n_vocab), dtype=torch.int8, device=dev)
+        _lib.call("iw_classifier", hl.data_ptr(), dec.token_embedding.weight.data_ptr(), sc["cm"],
+                  sc["cs"], logits.data_ptr(), B, C, dec.n_vocab, _stream())
+        self.last_logits = logits
+        if next_out is None:
+            next_out = torch.empty(B, dtype=torch.int64, device=dev)
+        _lib.call("iw_argmax_rows", logits.data_ptr(), B, dec.n_vocab, dec.n_vocab, next_out.data_ptr(),
+                  _stream())
+        self.offset = Tk
+        return next_out
+
+
+def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torch.Tensor,
+                  steps: int, runner: Optional[DecoderRunner] = None,
+                  keep_logits: bool = False):
+    """Fixed-step greedy decoding; returns int64 tokens [B, prompt_len + steps] (and the int8
+    logits of every step [B, steps, vocab] when ``keep_logits``)."""
+    B, P = prompt.shape
+    dec = model.decoder
+    if P + steps > dec.n_ctx:
+        raise ValueError(f"prompt + steps exceeds n_text_ctx ({dec.n_ctx})")
+    if int(prompt.min()) < 0 or int(prompt.max()) >= dec.n_vocab:
+        raise ValueError("prompt token id out of range")
+    if runner is None:
+        runner = DecoderRunner(dec, B, audio_features.shape[1])
+    runner.set_audio(audio_features)
+    out = torch.empty((P + steps, B), dtype=torch.int64, device=prompt.device)
+    out[:P] = prompt.t()
+    logits: List[torch.Tensor] = []
+    cur = prompt.contiguous()
+    for i in range(steps):
+        runner.step(cur, out[P + i])
+        if keep_logits:
+            logits.append(runner.last_logits.clone())
+        cur = out[P + i]
+    toks = out.t().contiguous()
+    if keep_logits:
+        return toks, torch.stack(logits, 1)
+    return toks

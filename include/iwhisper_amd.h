@@ -218,6 +218,19 @@ int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, i
                  uint8_t av_multiplier, int8_t av_shift, uint32_t rsqrt_offset,
                  const uint8_t *table, bool decode, iw_stream_t stream);
 
+/* Layout helpers for the KV caches (the reference's view/permute/.contiguous()
+ * copies and hook-side torch.cat, model_int.py:842-949 and 1604-1610):
+ * transpose_heads writes dst[b][h][d][t_offset+t] = src[b*src_sb + t*src_st + h*D + d]
+ * (V^T per head); copy_rows writes dst[b*dst_sb + (t_offset+t)*dst_st + c] =
+ * src[b*src_sb + t*src_st + c] for c < channels. */
+int iw_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                       int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_offset,
+                       int64_t batch, int64_t positions, int64_t heads, int64_t head_dim,
+                       iw_stream_t stream);
+int iw_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst, int64_t dst_sb,
+                 int64_t dst_st, int64_t t_offset, int64_t batch, int64_t positions,
+                 int64_t channels, iw_stream_t stream);
+
 /* First index of the maximum of each row of int8 logits (greedy decoding,
  * decoding.py:280-296 on the int8 logits, which dequantisation by a positive
  * scale does not reorder). x [rows, ld], out [rows] int64. */
