@@ -1,0 +1,200 @@
+"""Throughput of the integer Whisper encoder + greedy decoder on one MI355X.
+
+Workload (default): Whisper-large shapes, full integer encoder + decoder,
+batch 128 of seeded 30 s log-mels (128 x 3000), 445-step greedy decode after the
+3-token start prompt (448-token context), random-init weights calibrated into
+an integer checkpoint. One step = encoder over the batch + the whole greedy
+decode; inputs are resident in HBM before the timed region.
+
+Prints one JSON line: end-to-end audio-seconds/s as ``value``, plus encoder
+audio-s/s, decoder tokens/s, the encoder-GEMM int8 MFMA roofline fraction
+(HIP events around every encoder GEMM launch in the timed steps) and the CPU
+oracle timed on a bounded sample on the host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "encoder audio-sec/sec + decoder tokens/sec, large shapes; % int8 MFMA peak"
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (shape, batch, decode steps, description)
+    "large": ("large", 128, 445, "Whisper-large shapes (d=1280, 20 heads, 32+32 layers, 128 mels), "
+              "integer encoder + greedy decoder, batch 128, 445 greedy steps after a 3-token prompt "
+              "(448-token context)"),
+    "medium": ("medium", 64, 221, "Whisper-medium shapes, batch 64, 221 greedy steps"),
+    "small": ("small", 32, 128, "Whisper-small shapes, batch 32, 128 greedy steps"),
+    "base-encoder": ("base", 16, 0, "Whisper-base shapes, integer encoder only, batch 16"),
+    "tiny": ("tiny", 1, 32, "Whisper-tiny shapes (4 heads), batch 1, 32 greedy steps"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: int = 4,
+                 dec_steps: int = 12) -> dict:
+    """The oracle on the host for one sample: the encoder front end, ``enc_blocks``
+    of the encoder blocks and ``dec_steps`` greedy steps, scaled to the full
+    per-sample workload (all blocks, all steps)."""
+    import numpy as np
+    from oracle.model_oracle import OracleWhisper
+
+    ref = OracleWhisper(dims, params, threads=threads)
+    mel = iw.synth.synthetic_mel(1, dims.n_mels, 2 * dims.n_audio_ctx, seed=99)
+    t0 = time.perf_counter()
+    x = ref.encoder_frontend(mel)
+    t1 = time.perf_counter()
+    nb = min(enc_blocks, dims.n_audio_layer)
+    for i in range(nb):
+        x = ref._block(x, None, None, None, f"encoder.blocks.{i}", dims.n_audio_head, False)
+    t2 = time.perf_counter()
+    xa = ref._ln(x, "encoder.ln_post")
+    t3 = time.perf_counter()
+    enc = (t1 - t0) + (t2 - t1) * dims.n_audio_layer / max(nb, 1) + (t3 - t2)
+    dec = 0.0
+    nd = min(dec_steps, steps_total)
+    if nd:
+        prompt = iw.synth.prompt_tokens(1, dims.n_vocab)
+        t4 = time.perf_counter()
+        ref.greedy(xa, prompt, nd)
+        dec = (time.perf_counter() - t4) * steps_total / nd
+    return {
+        "value": round(30.0 / (enc + dec), 5), "unit": "audio-s/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle (oracle/iw_oracle.c, OpenMP GEMM/attention loops) on one 30 s sample: "
+                   f"encoder front end + {nb}/{dims.n_audio_layer} blocks scaled to all blocks, "
+                   f"{nd}/{steps_total} greedy steps scaled to all steps; "
+                   f"measured {t3 - t0 + (dec * nd / max(steps_total, 1)):.1f} s"),
+        "encoder_s_per_sample": round(enc, 3), "decoder_s_per_sample": round(dec, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="large", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--decode-steps", type=int, default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested). Data parallelism over the batch is described in "
+              f"DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import __graft_entry__
+
+    iw = __graft_entry__.load_package()
+    shape, batch, dsteps, desc = WORKLOADS[args.workload]
+    batch = args.batch or batch
+    dsteps = dsteps if args.decode_steps is None else args.decode_steps
+    dims = iw.SHAPES[shape]
+    if 3 + dsteps > dims.n_text_ctx:
+        raise SystemExit("decode steps exceed the 448-token context")
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    t0 = time.time()
+    params = iw.synth.calibrated_int_params(dims, seed=0)
+    log(f"[bench] synthetic checkpoint ({iw.synth.param_bytes(params) / 1e9:.2f} GB) "
+        f"in {time.time() - t0:.1f} s")
+    model = iw.Whisper_int.from_params(dims, params).cuda().eval()
+    mel = torch.from_numpy(iw.synth.synthetic_mel(batch, dims.n_mels, 2 * dims.n_audio_ctx, seed=1)).cuda()
+    prompt = torch.from_numpy(iw.synth.prompt_tokens(batch, dims.n_vocab)).cuda()
+    enc = iw.EncoderRunner(model.encoder, batch)
+    dec = iw.DecoderRunner(model.decoder, batch, dims.n_audio_ctx) if dsteps else None
+    torch.cuda.synchronize()
+    log(f"[bench] model on GPU, batch {batch}, {dsteps} decode steps")
+
+    def step(timed: bool):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e2 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        feats = enc(mel)
+        e1.record()
+        toks = iw.greedy_decode(model, feats, prompt, dsteps, runner=dec) if dsteps else None
+        e2.record()
+        return e0, e1, e2, toks
+
+    with torch.no_grad():
+        for w in range(args.warmup):
+            step(False)
+            torch.cuda.synchronize()
+            log(f"[bench] warmup {w + 1}/{args.warmup} done")
+        enc.timer = []
+        torch.cuda.synchronize()
+        t_start = time.perf_counter()
+        evs = []
+        for k in range(args.steps):
+            evs.append(step(True))
+            log(f"[bench] timed step {k + 1}/{args.steps} queued")
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t_start
+    enc_ms = sum(e0.elapsed_time(e1) for e0, e1, _, _ in evs)
+    dec_ms = sum(e1.elapsed_time(e2) for _, e1, e2, _ in evs)
+    K = args.steps
+    ms_per_step = wall * 1000.0 / K
+    audio_s = 30.0 * batch
+    value = audio_s * K / wall
+    gemm = [(ops, s.elapsed_time(e)) for kind, ops, s, e in enc.timer if kind == "gemm"]
+    attn = [(ops, s.elapsed_time(e)) for kind, ops, s, e in enc.timer if kind == "attention"]
+    g_ops = sum(o for o, _ in gemm) / len(gemm)
+    g_ms = sum(t for _, t in gemm) / len(gemm)
+    g_tops = g_ops / (g_ms * 1e-3) / 1e12
+    a_tops = (sum(o for o, _ in attn) / max(sum(t for _, t in attn), 1e-9)) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "audio-s/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded log-mel N(-0.5,0.4) clipped to [-1.5,1.5]; random-init N(0,0.02) "
+                "weights calibrated to an integer checkpoint)",
+        "config": {"workload": desc, "shape": shape, "global_batch": batch, "seq_len": dims.n_audio_ctx,
+                   "decode_steps": dsteps, "parallelism": "none"},
+        "encoder_audio_s_per_s": round(audio_s * K / (enc_ms / 1000.0), 2),
+        "decoder_tokens_per_s": round(batch * dsteps * K / (dec_ms / 1000.0), 1) if dsteps else None,
+        "encoder_ms_per_step": round(enc_ms / K, 3),
+        "decoder_ms_per_step": round(dec_ms / K, 3),
+        "encoder_attention_tops": round(a_tops, 1),
+        "roofline": {"bound": "mfma", "kernel": "gemm_i8_kernel (encoder QKV/out/FC1/FC2 launches)",
+                     "achieved": round(g_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                     "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4)},
+    }
+    del model, enc, dec
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
+        t0 = time.time()
+        result["cpu_baseline"] = cpu_baseline(iw, dims, params, dsteps, threads)
+        log(f"[bench] cpu baseline in {time.time() - t0:.1f} s")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

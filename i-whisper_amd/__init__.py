@@ -15,7 +15,7 @@ from .runtime import DecoderRunner, EncoderRunner, greedy_decode  # noqa: F401
 
 # Whisper model shapes (n_mels, n_audio_ctx, d, heads, layers, vocab, n_text_ctx)
 SHAPES = {
-    "tiny": ModelDimensions(80, 1500, 384, 6, 4, 51865, 448, 384, 6, 4),
+    "tiny": ModelDimensions(80, 1500, 384, 4, 4, 51865, 448, 384, 4, 4),  # 4 heads as the CPU case
     "base": ModelDimensions(80, 1500, 512, 8, 6, 51865, 448, 512, 8, 6),
     "small": ModelDimensions(80, 1500, 768, 12, 12, 51865, 448, 768, 12, 12),
     "medium": ModelDimensions(80, 1500, 1024, 16, 24, 51865, 448, 1024, 16, 24),

@@ -111,6 +111,22 @@ class EncoderRunner:
         self.f8 = torch.empty((self.M, 4 * C), dtype=torch.int8, device=dev)
         self.out = torch.empty((batch, T, C), dtype=torch.int8, device=dev)
         self.tables = [b.attn.shift_exp_table() for b in encoder.blocks]
+        # Optional per-launch timing: a list receiving (kind, ops, start, end)
+        # HIP events recorded on the launch stream around GEMM / attention calls.
+        self.timer: Optional[list] = None
+
+    def _tick(self, kind: str, ops: float):
+        if self.timer is None:
+            return None
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return kind, ops, e
+
+    def _tock(self, tok):
+        if tok is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.timer.append((*tok, e))
 
     def block(self, i: int, x16: torch.Tensor):
         blk = self.enc.blocks[i]
@@ -119,18 +135,28 @@ class EncoderRunner:
         sc = blk._scalars()
         B, C, H, D, T, M = self.B, self.C, self.H, self.D, self.T, self.M
         _ln(blk.attn_ln, x16, M, self.h8)
+        t = self._tick("gemm", 2.0 * M * 3 * C * C)
         self.qkv[i].linear8(self.h8, M, self.qkv_buf)
+        self._tock(t)
         q = self.qkv_buf.data_ptr()
         _lib.call("iw_transpose_heads", q + 2 * C, T * 3 * C, 3 * C, self.vt.data_ptr(),
                   H * D * self.tp, D * self.tp, self.tp, 0, B, T, H, D, _stream())
+        t = self._tick("attention", 4.0 * B * H * T * T * D)
         _lib.call("iw_attention", q, T * 3 * C, 3 * C, q + C, T * 3 * C, D, 3 * C,
                   self.vt.data_ptr(), H * D * self.tp, D * self.tp, self.tp, self.wv.data_ptr(),
                   T * C, C, None, B, H, T, T, D, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
                   att.rsqrt_offset, self.tables[i].data_ptr(), False, _stream())
+        self._tock(t)
+        t = self._tick("gemm", 2.0 * M * C * C)
         _lin32_res(att.out, self.wv.data_ptr(), M, x16, sc["a"])
+        self._tock(t)
         _ln(blk.mlp_ln, x16, M, self.h8)
+        t = self._tick("gemm", 2.0 * M * 4 * C * C)
         _mlp_gelu(blk, self.h8.data_ptr(), M, self.f8)
+        self._tock(t)
+        t = self._tick("gemm", 2.0 * M * 4 * C * C)
         _lin32_res(blk.mlp[2], self.f8.data_ptr(), M, x16, sc["m"])
+        self._tock(t)
 
     def __call__(self, mel: torch.Tensor) -> torch.Tensor:
         x16 = self.enc.frontend(mel)

@@ -57,10 +57,12 @@ def _sinusoids(length: int, channels: int, max_timescale: float = 10000.0) -> to
 
 class _Gen:
     def __init__(self, seed: int):
-        self.g = torch.Generator().manual_seed(seed)
+        self.r = np.random.default_rng(seed)
 
     def normal(self, *shape, std=0.02):
-        return torch.randn(*shape, generator=self.g) * std
+        a = self.r.standard_normal(shape, dtype=np.float32)
+        a *= np.float32(std)
+        return torch.from_numpy(a)
 
 
 def float_weights(dims: ModelDimensions, seed: int) -> Dict[str, torch.Tensor]:
@@ -276,14 +278,24 @@ def _linear(W, P, src: str, dst: str, alpha_in: float, alpha_out: float, kind: s
     if has_bias:
         b = torch.round(W[src + ".bias"].double() * alpha_in * aw).clamp(-2**31, 2**31 - 1)
         P[dst + ".bias"] = _np(b, np.int32)
-    mult = np.empty(aw.numel(), np.uint32)
-    shift = np.empty(aw.numel(), np.int8)
-    for n, a in enumerate(aw.tolist()):
-        r = alpha_out / (alpha_in * a)
-        m, s = _mulh_shift(r) if kind == "l8" else _mulh_lshift(r)
-        mult[n], shift[n] = m, s
-    P[dst + ".req_multiplier"] = mult
-    P[dst + ".req_shiftmount"] = shift
+    # vectorised _mulh_shift / _mulh_lshift over the output channels
+    r = alpha_out / (alpha_in * aw.cpu().numpy().astype(np.float64))
+    f, e = np.frexp(r)
+    m = np.round(f * 2.0 ** 32)
+    over = m >= 2.0 ** 32
+    m = np.where(over, m / 2, m)
+    e = e + over.astype(e.dtype)
+    if kind == "l8":
+        s = -e
+        sat = s < 0
+        m = np.where(sat, 2.0 ** 32 - 1, m)
+        s = np.minimum(np.where(sat, 0, s), 31)
+    else:
+        neg = e < 0
+        m = np.where(neg, np.maximum(1.0, np.round(m * 2.0 ** np.minimum(e, 0))), m)
+        s = np.where(neg, 0, np.minimum(e, 31))
+    P[dst + ".req_multiplier"] = m.astype(np.uint64).astype(np.uint32)
+    P[dst + ".req_shiftmount"] = s.astype(np.int8)
 
 
 def _layernorm(W, P, p: str, alpha_out: float):
