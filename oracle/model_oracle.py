@@ -20,10 +20,12 @@ from .oracle import Oracle
 
 
 class OracleWhisper:
-    def __init__(self, dims, params, threads: int = 8):
+    def __init__(self, dims, params, threads: int = 8, kind: str = "oracle"):
+        """``kind`` "oracle" composes oracle/iw_oracle.c; "ref" composes the reference's
+        own scalar kernels (oracle/_ref, where built) along the same dataflow."""
         self.d = dims
         self.P = params
-        self.o = Oracle("oracle", threads=threads)
+        self.o = Oracle(kind, threads=threads)
         n = dims.n_text_ctx
         self.mask = np.triu(np.ones((n, n), dtype=bool), 1)
 
