@@ -16,105 +16,17 @@
 // Integer sums are exact modulo 2^32 in any order, so the zero-point term
 // wz[n] * rowsum(A[m]) is formed from per-row sums taken with v_dot4 while
 // the A tile passes through registers, and added in the epilogue.
-#include "iw_common.hpp"
-#include "iw_gemm.hpp"
+#include "iw_gemm_dev.hpp"
 
 namespace iw {
+
+using namespace gemm;
 
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int LDT = BK + 16;  // LDS row stride in bytes
 constexpr int NT = 256;
-
-// Where the A tile comes from.
-enum AMode : int {
-  A_DENSE16 = 0,    // A[m][k] = a[m*lda + k], K % 16 == 0, 16-byte aligned rows
-  A_CONVCL16 = 1,   // channels-last conv input x[b][t][c], C % 16 == 0
-  A_GEN_DENSE = 2,  // any K / alignment, byte gathers
-  A_GEN_CONVNCT = 3 // conv input in [B][Cin][Tin] layout, byte gathers
-};
-
-// Byte-wise 16-byte chunk gather for the generic modes.
-__device__ __forceinline__ uint4 gather16(const GemmArgs &g, int amode, bool is_a, int64_t row,
-                                          int64_t k0) {
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
-  for (int i = 0; i < 16; ++i) {
-    int64_t k = k0 + i;
-    int32_t v = 0;
-    if (k < g.K) {
-      if (!is_a) {
-        if (row < g.N) v = (uint8_t)g.b[row * g.ldb + k];
-      } else if (amode == A_GEN_DENSE) {
-        if (row < g.M) v = (uint8_t)g.a[row * g.lda + k];
-      } else {  // A_GEN_CONVNCT: k = ic * ksize + kk
-        if (row < g.M) {
-          int64_t bb = row / g.conv_tout, t = row % g.conv_tout;
-          int64_t ic = k / g.conv_ksize, kk = k % g.conv_ksize;
-          int64_t pos = t * g.conv_stride - g.conv_pad + kk;
-          if (pos >= 0 && pos < g.conv_tin)
-            v = (uint8_t)g.a[(bb * g.conv_cin + ic) * g.conv_tin + pos];
-        }
-      }
-    }
-    w[i >> 2] |= (uint32_t)v << (8 * (i & 3));
-  }
-  return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-struct RowInfo {
-  const int8_t *base;  // address of element k = 0 of this row (may be out of range)
-  int32_t pos0;        // conv: first input position t*stride - pad
-  bool valid;
-};
-
-__device__ __forceinline__ RowInfo a_row_info(const GemmArgs &g, int amode, int64_t m) {
-  RowInfo r;
-  r.valid = m < g.M;
-  r.pos0 = 0;
-  r.base = g.a;
-  if (amode == A_DENSE16) {
-    r.base = g.a + m * g.lda;
-  } else if (amode == A_CONVCL16 && r.valid) {
-    int64_t bb = m / g.conv_tout, t = m % g.conv_tout;
-    r.pos0 = (int32_t)(t * g.conv_stride - g.conv_pad);
-    r.base = g.a + (bb * g.conv_tin + r.pos0) * (int64_t)g.conv_cin;
-  }
-  return r;
-}
-
-__device__ __forceinline__ uint4 load_a16(const GemmArgs &g, int amode, const RowInfo &r,
-                                          int64_t m, int64_t k) {
-  if (amode == A_DENSE16) {
-    if (r.valid && k < g.K) return *reinterpret_cast<const uint4 *>(r.base + k);
-    return make_uint4(0, 0, 0, 0);
-  }
-  if (amode == A_CONVCL16) {
-    if (r.valid && k < g.K) {
-      int32_t pos = r.pos0 + (int32_t)(k / g.conv_cin);
-      if (pos >= 0 && pos < g.conv_tin) return *reinterpret_cast<const uint4 *>(r.base + k);
-    }
-    return make_uint4(0, 0, 0, 0);
-  }
-  return gather16(g, amode, true, m, k);
-}
-
-__device__ __forceinline__ uint4 load_b16(const GemmArgs &g, bool fast, int64_t n, int64_t k) {
-  if (fast) {
-    if (n < g.N && k < g.K) return *reinterpret_cast<const uint4 *>(g.b + n * g.ldb + k);
-    return make_uint4(0, 0, 0, 0);
-  }
-  return gather16(g, A_GEN_DENSE, false, n, k);
-}
-
-__device__ __forceinline__ int32_t sum16(uint4 v) {
-  const int ones = 0x01010101;
-  int32_t s = __builtin_amdgcn_sdot4((int)v.x, ones, 0, false);
-  s = __builtin_amdgcn_sdot4((int)v.y, ones, s, false);
-  s = __builtin_amdgcn_sdot4((int)v.z, ones, s, false);
-  s = __builtin_amdgcn_sdot4((int)v.w, ones, s, false);
-  return s;
-}
 
 // Linear32 output: low 32 bits of mulh(acc, m) * 2^shift; 0 outside [0, 31].
 __device__ __forceinline__ int32_t linear32_out(int32_t acc, uint32_t m, int32_t s) {
@@ -307,6 +219,8 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 int gemm_dense(const GemmArgs &g, hipStream_t s) {
   const bool afast = g.K % 16 == 0 && g.lda % 16 == 0 && aligned16(g.a);
   const bool bfast = g.K % 16 == 0 && g.ldb % 16 == 0 && aligned16(g.b);
+  if (g.M >= kBigGemmMinRows && gemm_dtl_eligible(g)) return gemm_dtl(g, s);
+  if (afast && bfast && g.M >= kBigGemmMinRows) return gemm_big(g, false, s);
   switch (g.epi) {
     case EPI_L8:
       if (afast && bfast) return launch<A_DENSE16, true, EPI_L8, OUT_ROW>(g, s);
@@ -331,6 +245,7 @@ int gemm_conv(const GemmArgs &g, bool channels_last, hipStream_t s) {
     const bool fast = g.conv_cin % 16 == 0 && aligned16(g.a) && g.K % 16 == 0 &&
                       g.ldb % 16 == 0 && aligned16(g.b);
     if (!fast) return fail("channels-last conv needs Cin % 16 == 0 and 16-byte aligned buffers");
+    if (g.M >= kBigGemmMinRows) return gemm_big(g, true, s);
     return launch<A_CONVCL16, true, EPI_S8, OUT_ROW>(g, s);
   }
   return launch<A_GEN_CONVNCT, false, EPI_S8, OUT_NCT>(g, s);

@@ -59,7 +59,14 @@ struct GemmArgs {
   int64_t out_T = 1;  // OUT_NCT: rows are (b, t) with t in [0, out_T)
 };
 
+// Rows from which the 256 x 128 tile kernel (iw_gemm_big.hip) is used.
+constexpr int64_t kBigGemmMinRows = 8192;
+
 int gemm_dense(const GemmArgs &g, hipStream_t s);
+int gemm_big(const GemmArgs &g, bool conv_cl, hipStream_t s);
+// Direct-to-LDS kernel (iw_gemm_dtl.hip): dense A, K % 64 == 0, 16-byte aligned.
+bool gemm_dtl_eligible(const GemmArgs &g);
+int gemm_dtl(const GemmArgs &g, hipStream_t s);
 int gemm_conv(const GemmArgs &g, bool channels_last, hipStream_t s);
 
 }  // namespace iw
