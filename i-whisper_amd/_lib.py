@@ -48,6 +48,14 @@ SIGNATURES = {
     "iw_argmax_rows": [_p, _i64, _i64, _i64, _p, _p],
     "iw_transpose_heads": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "iw_copy_rows": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "iw_gather_heads": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "iw_linear8_qkv_cache": [_p, _p, _p, _p, _p, _p, _i64, _i64, _b, _b, _p, _i64, _p, _i64, _i64,
+                             _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "iw_attention_decode_cache": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
+                                  _i64, _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32,
+                                  _p],
+    "iw_embed_tokens": [_p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _p],
+    "iw_greedy_advance": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p],
 }
 
 _lock = threading.Lock()

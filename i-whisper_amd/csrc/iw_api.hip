@@ -459,8 +459,8 @@ int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, i
     return launch_attn_decode(a, as_stream(stream));
   }
   IW_REQUIRE(table, "prefill attention needs the shift-exp table");
-  IW_REQUIRE(v_sh == head_dim * v_sd && v_sb == heads * head_dim * v_sd && k_sh == head_dim,
-             "prefill attention expects V^T as [B,H,D,v_sd] and K as [B,T,H*D]");
+  IW_REQUIRE(v_sh == head_dim * v_sd && v_sb == heads * head_dim * v_sd,
+             "prefill attention expects V^T as [B,H,D,v_sd]");
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess) {
     int v = 0;
@@ -483,6 +483,22 @@ int iw_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t
                                 positions, heads, head_dim, as_stream(stream));
 }
 
+int iw_gather_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst, int64_t dst_sb,
+                    int64_t dst_sh, int64_t dst_st, int64_t t_offset, int64_t batch,
+                    int64_t positions, int64_t heads, int64_t head_dim, iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && positions >= 0 && heads > 0 && head_dim > 0 && t_offset >= 0,
+             "invalid gather shape");
+  IW_REQUIRE(head_dim % 16 == 0, "gather_heads needs head_dim % 16 == 0");
+  if (batch * positions == 0) return IW_OK;
+  IW_REQUIRE(src && dst, "null tensor pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) |
+                          (uintptr_t)src_sb | (uintptr_t)src_st | (uintptr_t)dst_sb |
+                          (uintptr_t)dst_sh | (uintptr_t)dst_st;
+  IW_REQUIRE((align & 15) == 0, "gather_heads operands must be 16-byte aligned");
+  return launch_gather_heads(src, src_sb, src_st, dst, dst_sb, dst_sh, dst_st, t_offset, batch,
+                             positions, heads, head_dim, as_stream(stream));
+}
+
 int iw_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst, int64_t dst_sb,
                  int64_t dst_st, int64_t t_offset, int64_t batch, int64_t positions,
                  int64_t channels, iw_stream_t stream) {
@@ -491,6 +507,124 @@ int iw_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
   IW_REQUIRE(src && dst, "null tensor pointer");
   return launch_copy_rows(src, src_sb, src_st, dst, dst_sb, dst_st, t_offset, batch, positions,
                           channels, as_stream(stream));
+}
+
+int iw_linear8_qkv_cache(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                         const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                         int64_t M, int64_t K, bool has_bias, bool asymmetric, int8_t *q_out,
+                         int64_t q_ld, int8_t *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                         int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
+                         int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
+                         const int32_t *pos, iw_stream_t stream) {
+  const int64_t N = 3 * channels;
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N, has_bias,
+                        asymmetric);
+  if (rc) return rc;
+  if (M == 0) return IW_OK;
+  IW_REQUIRE(M <= kSkinnyMaxRows, "the KV-cache QKV projection takes at most 128 rows");
+  IW_REQUIRE(channels > 0 && head_dim > 0 && channels % head_dim == 0, "invalid head geometry");
+  IW_REQUIRE(channels <= 0x3fffffff && tokens_per_row_group > 0 && M % tokens_per_row_group == 0,
+             "rows must be whole groups of tokens_per_row_group");
+  IW_REQUIRE(k_cache && v_cache && pos, "null cache pointer");
+  IW_REQUIRE(cache_positions > 0 && cache_positions <= 0x7fffffff && cache_positions <= v_sd,
+             "cache_positions must be positive and fit the transposed V rows");
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N,
+                           has_bias, asymmetric, EPI_L8);
+  IW_REQUIRE(gemm_skinny_eligible(g), "QKV projection needs K % 16 == 0 and 16-byte aligned operands");
+  SkinnyScatter sc;
+  sc.q = q_out;
+  sc.ldq = q_ld;
+  sc.k = k_cache;
+  sc.k_sb = k_sb;
+  sc.k_sh = k_sh;
+  sc.k_st = k_st;
+  sc.v = v_cache;
+  sc.v_sb = v_sb;
+  sc.v_sh = v_sh;
+  sc.v_sd = v_sd;
+  sc.C = (int)channels;
+  sc.D = (int)head_dim;
+  sc.T = (int)tokens_per_row_group;
+  sc.t_cap = (int)cache_positions;
+  sc.pos = pos;
+  return gemm_skinny(g, &sc, as_stream(stream));
+}
+
+int iw_attention_decode_cache(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
+                              int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
+                              int64_t v_sh, int64_t v_sd, int8_t *out, int64_t o_sb, int64_t batch,
+                              int64_t heads, int64_t head_dim, int64_t k_length,
+                              const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
+                              int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
+                              int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream) {
+  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
+  IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
+  IW_REQUIRE(head_dim == 64 || head_dim == 96 || head_dim == 128,
+             "decode attention supports head_dim 64, 96 and 128");
+  IW_REQUIRE(batch >= 0 && heads > 0 && k_length >= 0 && batch * heads <= 0x7fffffff,
+             "invalid attention shape");
+  // the key count on the device is k_length + *pos <= max_keys
+  IW_REQUIRE(max_keys >= k_length && max_keys <= kDecodeCacheMaxKeys && (pos || max_keys == k_length),
+             "at most 4096 keys, and max_keys bounds k_length + *pos");
+  IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((max_keys + 15) / 16) * 16,
+             "transposed V rows must be 16-byte multiples covering max_keys");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(q && k && vt && out, "null tensor pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(vt) | (uintptr_t)q_sb | (uintptr_t)k_sb |
+                          (uintptr_t)k_sh | (uintptr_t)k_st | (uintptr_t)v_sb | (uintptr_t)v_sh;
+  IW_REQUIRE((align & 15) == 0, "decode attention operands must be 16-byte aligned");
+  AttnArgs a;
+  a.q = q;
+  a.q_sb = q_sb;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_st = k_st;
+  a.vt = vt;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sd = v_sd;
+  a.vt_ld = v_sd;
+  a.out = out;
+  a.o_sb = o_sb;
+  a.B = (int32_t)batch;
+  a.H = (int32_t)heads;
+  a.Tq = 1;
+  a.Tk = (int32_t)k_length;
+  a.D = (int32_t)head_dim;
+  a.qk_m = qk_multiplier;
+  a.qk_s = (uint32_t)(qk_shift > 0 ? qk_shift : 0);
+  a.frac_bits = frac_bits;
+  a.av_m = av_multiplier;
+  a.av_s = (uint32_t)(av_shift < 0 ? 0 : (av_shift > 32 ? 32 : av_shift));
+  a.rsqrt_off = rsqrt_offset;
+  a.max_tk = (int32_t)max_keys;
+  return launch_attn_decode_cache(a, pos, as_stream(stream));
+}
+
+int iw_embed_tokens(const int64_t *tokens, const int8_t *table, const int8_t *pe,
+                    int64_t pe_rows, const int32_t *pos, const uint16_t *multiplier,
+                    const int8_t *shift, int16_t *out, int64_t batch, int64_t channels,
+                    iw_stream_t stream) {
+  IW_REQUIRE(batch >= 0 && channels > 0 && pe_rows > 0, "invalid embedding shape");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(tokens && table && pe && pos && multiplier && shift && out, "null tensor pointer");
+  return launch_add_requant15(table, tokens, pe, multiplier, shift, out, batch, 1, channels, 0, 0,
+                              as_stream(stream), pos, pe_rows);
+}
+
+int iw_greedy_advance(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld,
+                      int64_t *next_tokens, int64_t *history, int64_t history_ld,
+                      int64_t history_cols, int32_t *step, int32_t *pos, int32_t pos_increment,
+                      iw_stream_t stream) {
+  IW_REQUIRE(rows >= 0 && cols > 0 && ld >= cols && history_cols > 0 && history_ld >= history_cols,
+             "invalid greedy step shape");
+  IW_REQUIRE(logits && next_tokens && history && step && pos, "null tensor pointer");
+  int rc = rows ? launch_argmax_rows(logits, rows, cols, ld, next_tokens, as_stream(stream)) : 0;
+  if (rc) return rc;
+  return launch_greedy_record(next_tokens, history, rows, history_ld, history_cols, step, pos,
+                              pos_increment, as_stream(stream));
 }
 
 int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,

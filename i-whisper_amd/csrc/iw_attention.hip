@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
     const int h = (int)(bh % a.H);
     const int64_t b = bh / a.H;
     const int q = qt * 128 + wave * 32 + ql;  // this lane's query row
-    const int8_t *kbase = a.k + b * a.k_sb + (int64_t)h * D;
+    const int8_t *kbase = a.k + b * a.k_sb + (int64_t)h * a.k_sh;
     const int8_t *vbase = a.vt + (b * a.H + h) * (int64_t)D * a.vt_ld;
 
     v4i qf[KS];
@@ -438,6 +438,149 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
   }
 }
 
+
+// ------------------------------------------------------------------------
+// Decode attention over per-head KV caches (one query row per (batch, head))
+// ------------------------------------------------------------------------
+//
+// K cache [B, H, T_cap, D] (rows of D bytes contiguous per head), V cache
+// transposed [B, H, D, T_cap16]. The key count is k_length, plus *pos when
+// pos is given (the self-attention cache length lives on the device, so a
+// captured decode step can be replayed). One block of 256 threads per
+// (batch, head):
+//   1. scores: LPK lanes share a key (16 bytes each), so one wave load reads
+//      64 / LPK consecutive keys; raw int32 scores go to LDS and their max
+//      gives the row max (the requant is monotone);
+//   2. P = shift_exp(requant(s) - row_max - 1) to LDS, with its row sum;
+//   3. O[d] = sum_j P[j] V^T[d][j]: each wave owns D / 4 rows of V^T and its
+//      lanes walk a row's 16-byte chunks, so each wave load reads 1 KB of one
+//      row; the per-lane partial sums are reduced once per row.
+constexpr int DC_MAX_TK = 4096;
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, const int32_t *pos) {
+  constexpr int CPK = D / 16;                      // 16-byte chunks per key
+  constexpr int LPK = CPK <= 4 ? 4 : 8;            // lanes per key
+  constexpr int KPW = 64 / LPK;                    // keys per wave load
+  constexpr int RPW = D / 4;                       // V^T rows per wave
+  __shared__ int32_t sS[DC_MAX_TK];
+  __shared__ __attribute__((aligned(16))) uint8_t sP[DC_MAX_TK];
+  __shared__ int32_t sRed[4];
+  __shared__ uint32_t sSum[4];
+  __shared__ uint32_t sHi;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t bh = blockIdx.x;
+  const int h = (int)(bh % a.H);
+  const int64_t b = bh / a.H;
+  const int Tk = min(a.Tk + (pos ? *pos : 0), a.max_tk);
+  if (tid == 0) sHi = 0;
+
+  // ---- phase 1: raw scores ----
+  const int chunk = lane % LPK;
+  const bool cvalid = chunk < CPK;
+  v4i qv = v4i{0, 0, 0, 0};
+  if (cvalid)
+    qv = *reinterpret_cast<const v4i *>(a.q + b * a.q_sb + (int64_t)h * D + chunk * 16);
+  const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh;
+  int32_t mx = INT32_MIN;
+  for (int j0 = wave * KPW; j0 < Tk; j0 += 4 * KPW) {
+    const int j = j0 + lane / LPK;
+    int32_t acc = 0;
+    if (j < Tk && cvalid) {
+      const v4i kv = *reinterpret_cast<const v4i *>(kb + (int64_t)j * a.k_st + chunk * 16);
+      acc = __builtin_amdgcn_sdot4(qv[0], kv[0], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[1], kv[1], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[2], kv[2], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[3], kv[3], acc, false);
+    }
+#pragma unroll
+    for (int o = 1; o < LPK; o <<= 1) acc += __shfl_xor(acc, o);
+    if (j < Tk) {
+      if (chunk == 0) sS[j] = acc;
+      mx = max(mx, acc);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  if (lane == 0) sRed[wave] = mx;
+  __syncthreads();
+  mx = max(max(sRed[0], sRed[1]), max(sRed[2], sRed[3]));
+  const int32_t rowmax = mx == INT32_MIN ? -32768 : qk_requant16(mx, a.qk_m, a.qk_s);
+  const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
+
+  // ---- phase 2: P and its row sum ----
+  const int tk16 = (Tk + 15) & ~15;
+  uint32_t psum = 0, hi = 0;
+  for (int j = tid; j < tk16; j += 256) {
+    uint32_t p = 0;
+    if (j < Tk) {
+      const int32_t h16 = qk_requant16(sS[j], a.qk_m, a.qk_s);
+      // x_sub = qk - rmp1 modulo 2^16
+      p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)h16 - rmp1), a.frac_bits);
+    }
+    sP[j] = (uint8_t)p;
+    psum += p;
+    hi |= p;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) psum += (uint32_t)__shfl_xor((int)psum, off);
+  if (lane == 0) sSum[wave] = psum;
+  if (hi & 0x80u) atomicOr(&sHi, 1u);
+  __syncthreads();
+  const int32_t total = (int32_t)(sSum[0] + sSum[1] + sSum[2] + sSum[3]);
+  const int32_t inv = fisr(total, a.rsqrt_off);
+  const bool any_hi = sHi != 0;
+
+  // ---- phase 3: O = P . V^T ----
+  const int nch = tk16 >> 4;
+  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)(wave * RPW) * a.v_sd;
+  uint32_t accd[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) accd[r] = 0;
+  for (int c = lane; c < nch; c += 64) {
+    const uint4 pv = reinterpret_cast<const uint4 *>(sP)[c];
+    const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const uint4 vv = *reinterpret_cast<const uint4 *>(vb + (int64_t)r * a.v_sd + c * 16);
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+      if (!any_hi) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          accd[r] = (uint32_t)__builtin_amdgcn_sdot4((int)pw[e], (int)vw[e], (int)accd[r], false);
+      } else {
+        // P = 128 only after an int16 row-max wrap: split off the top bit
+        int32_t hs = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          accd[r] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw[e] & 0x7f7f7f7fu), (int)vw[e],
+                                                     (int)accd[r], false);
+          hs = __builtin_amdgcn_sdot4((int)((pw[e] >> 7) & 0x01010101u), (int)vw[e], hs, false);
+        }
+        accd[r] += (uint32_t)hs << 7;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    uint32_t v = accd[r];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off);
+    accd[r] = v;
+  }
+  if (lane < RPW) {
+    uint32_t accv = 0;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      if (r == lane) accv = accd[r];
+    const int d = wave * RPW + lane;
+    int32_t y = rshift((int32_t)(accv * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+    a.out[b * a.o_sb + (int64_t)h * D + d] = (int8_t)clampi(y, -127, 127);
+  }
+}
 }  // namespace
 
 int launch_qk_requant_rowmax(const int8_t *q, const int8_t *k, const uint8_t *mask, int16_t *qk,
@@ -497,6 +640,27 @@ int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s) {
   }
 #undef IW_PF
   return check_launch("attn_prefill_kernel");
+}
+
+int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s) {
+  if ((int64_t)a.B * a.H == 0) return 0;
+  switch (a.D) {
+    case 64:
+      hipLaunchKernelGGL(attn_decode_cache_kernel<64>, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a,
+                         pos);
+      break;
+    case 96:
+      hipLaunchKernelGGL(attn_decode_cache_kernel<96>, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a,
+                         pos);
+      break;
+    case 128:
+      hipLaunchKernelGGL(attn_decode_cache_kernel<128>, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s,
+                         a, pos);
+      break;
+    default:
+      return fail("decode attention supports head_dim 64, 96 and 128");
+  }
+  return check_launch("attn_decode_cache_kernel");
 }
 
 int launch_attn_decode(const AttnArgs &a, hipStream_t s) {

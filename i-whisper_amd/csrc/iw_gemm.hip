@@ -219,6 +219,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 int gemm_dense(const GemmArgs &g, hipStream_t s) {
   const bool afast = g.K % 16 == 0 && g.lda % 16 == 0 && aligned16(g.a);
   const bool bfast = g.K % 16 == 0 && g.ldb % 16 == 0 && aligned16(g.b);
+  if (gemm_skinny_eligible(g)) return gemm_skinny(g, nullptr, s);
   if (g.M >= kBigGemmMinRows && gemm_dtl_eligible(g)) return gemm_dtl(g, s);
   if (afast && bfast && g.M >= kBigGemmMinRows) return gemm_big(g, false, s);
   switch (g.epi) {

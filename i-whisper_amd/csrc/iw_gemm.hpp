@@ -59,6 +59,27 @@ struct GemmArgs {
   int64_t out_T = 1;  // OUT_NCT: rows are (b, t) with t in [0, out_T)
 };
 
+// Decode-step QKV projection: the epilogue writes Q (columns [0, C)) to
+// q[m][n], and appends K / V (columns [C, 2C) / [2C, 3C), head h = c / D,
+// d = c % D) of row m = b * T + i at cache position t = *pos + i:
+// K to k[b*k_sb + h*k_sh + t*k_st + d], V to v[b*v_sb + h*v_sh + d*v_sd + t].
+struct SkinnyScatter {
+  int8_t *q = nullptr;
+  int64_t ldq = 0;
+  int8_t *k = nullptr;
+  int64_t k_sb = 0, k_sh = 0, k_st = 0;
+  int8_t *v = nullptr;
+  int64_t v_sb = 0, v_sh = 0, v_sd = 0;
+  int C = 0, D = 1, T = 1;
+  int t_cap = 0;  // cache positions; appends at t >= t_cap are dropped
+  const int32_t *pos = nullptr;
+};
+
+// Rows up to which the decode kernel (iw_gemm_skinny.hip) is used.
+constexpr int64_t kSkinnyMaxRows = 128;
+bool gemm_skinny_eligible(const GemmArgs &g);
+int gemm_skinny(const GemmArgs &g, const SkinnyScatter *scatter, hipStream_t s);
+
 // Rows from which the 256 x 128 tile kernel (iw_gemm_big.hip) is used.
 constexpr int64_t kBigGemmMinRows = 8192;
 

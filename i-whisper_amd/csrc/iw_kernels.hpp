@@ -31,6 +31,7 @@ struct AttnArgs {
   uint32_t av_s = 0;   // shift clamped to [0, 32]
   uint32_t rsqrt_off = 16;
   const uint8_t *lut = nullptr;  // IW_SEXP_LUT entries for frac_bits
+  int32_t max_tk = 0;            // decode over caches: bound of Tk + *pos
 };
 
 int layernorm_width_code(int64_t h);
@@ -45,7 +46,11 @@ int launch_residual15(const int32_t *br, const int16_t *res, uint16_t m, int16_t
                       hipStream_t s);
 int launch_add_requant15(const int8_t *x, const int64_t *tokens, const int8_t *addend,
                          const uint16_t *mult, const int8_t *shift, int16_t *out, int64_t batch,
-                         int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s);
+                         int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s,
+                         const int32_t *pos = nullptr, int64_t addend_rows = 0);
+int launch_greedy_record(const int64_t *next, int64_t *history, int64_t rows, int64_t hist_ld,
+                         int64_t hist_cols, int32_t *step, int32_t *pos, int32_t pos_inc,
+                         hipStream_t s);
 int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, int64_t m,
                         int64_t t, hipStream_t s);
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
@@ -53,6 +58,9 @@ int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, 
 int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
                            int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off,
                            int64_t B, int64_t T, int64_t H, int64_t D, hipStream_t s);
+int launch_gather_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                        int64_t dst_sb, int64_t dst_sh, int64_t dst_st, int64_t t_off, int64_t B,
+                        int64_t T, int64_t H, int64_t D, hipStream_t s);
 int launch_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
                      int64_t dst_sb, int64_t dst_st, int64_t t_off, int64_t B, int64_t T,
                      int64_t C, hipStream_t s);
@@ -69,5 +77,9 @@ int launch_pv_norm_requant(const uint8_t *p, const int8_t *v, const int32_t *row
 int launch_shift_exp_lut(uint8_t *lut, int32_t f, hipStream_t s);
 int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s);
 int launch_attn_decode(const AttnArgs &a, hipStream_t s);
+// Decode attention over [B,H,T_cap,D] / [B,H,D,T_cap16] caches; key count
+// a.Tk + *pos (pos may be null). At most 4096 keys.
+constexpr int kDecodeCacheMaxKeys = 4096;
+int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s);
 
 }  // namespace iw

@@ -152,12 +152,14 @@ __global__ void add_requant15_kernel(const int8_t *__restrict__ x, const int64_t
                                      const uint16_t *__restrict__ mult,
                                      const int8_t *__restrict__ shift, int16_t *__restrict__ out,
                                      int64_t positions, int64_t channels, int64_t total, int mpc,
-                                     int spc) {
+                                     int spc, const int32_t *__restrict__ pos, int64_t addend_rows) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  // with pos, addend rows start at the device-side position (clamped to the table)
+  const int64_t p0 = pos ? min(max((int64_t)*pos, (int64_t)0), addend_rows - positions) : 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t c = i % channels;
     const int64_t bt = i / channels;
-    const int64_t t = bt % positions;
+    const int64_t t = bt % positions + p0;
     const int32_t xv = tokens ? (int32_t)x[tokens[bt] * channels + c] : (int32_t)x[i];
     const int32_t v = xv + (int32_t)addend[t * channels + c];
     const int32_t p = (int32_t)((uint32_t)v * (uint32_t)mult[mpc ? c : 0]);
@@ -219,6 +221,23 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const int8_t *__restri
   if (threadIdx.x == 0) out[row] = si[0];
 }
 
+// Greedy step bookkeeping after argmax_rows wrote next[]: record the tokens
+// in column *step of the history and advance the device-side counters.
+__global__ void greedy_record_kernel(const int64_t *__restrict__ next, int64_t *__restrict__ history,
+                                     int64_t rows, int64_t hist_ld, int64_t hist_cols,
+                                     const int32_t *step) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t st = *step;
+  if (r < rows && st >= 0 && st < hist_cols) history[r * hist_ld + st] = next[r];
+}
+
+__global__ void greedy_advance_kernel(int32_t *step, int32_t *pos, int32_t pos_inc) {
+  if (threadIdx.x == 0) {
+    *step += 1;
+    *pos += pos_inc;
+  }
+}
+
 // Per-head transpose of a [B, T, H*D] operand slice into V^T layout:
 // dst[b][h][d][t_off + t] = src[b*src_sb + t*src_st + h*D + d].
 // Tiles of 64 positions x 64 feature columns go through LDS so that both the
@@ -244,6 +263,25 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(
       const int64_t h = c / D, d = c % D;
       dst[b * dst_sb + h * dst_sh + d * dst_sd + t_off + t] = tile[tx][r];
     }
+  }
+}
+
+// Per-head gather of a [B, T, H*D] operand slice into a [B, H, T_cap, D]
+// cache at positions [t_off, t_off + T): dst[b*dst_sb + h*dst_sh + (t_off+t)*dst_st + d]
+// = src[b*src_sb + t*src_st + h*D + d], 16 bytes per thread (D % 16 == 0).
+__global__ void gather_heads_kernel(const int8_t *__restrict__ src, int64_t src_sb, int64_t src_st,
+                                    int8_t *__restrict__ dst, int64_t dst_sb, int64_t dst_sh,
+                                    int64_t dst_st, int64_t t_off, int64_t B, int64_t T, int64_t H,
+                                    int64_t D) {
+  const int64_t cpr = H * D / 16;  // 16-byte chunks per source row
+  const int64_t total = B * T * cpr;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % cpr, bt = i / cpr;
+    const int64_t t = bt % T, b = bt / T;
+    const int64_t h = (c * 16) / D, d = (c * 16) % D;
+    *reinterpret_cast<uint4 *>(dst + b * dst_sb + h * dst_sh + (t_off + t) * dst_st + d) =
+        *reinterpret_cast<const uint4 *>(src + b * src_sb + t * src_st + c * 16);
   }
 }
 
@@ -319,11 +357,12 @@ int launch_residual15(const int32_t *br, const int16_t *res, uint16_t m, int16_t
 
 int launch_add_requant15(const int8_t *x, const int64_t *tokens, const int8_t *addend,
                          const uint16_t *mult, const int8_t *shift, int16_t *out, int64_t batch,
-                         int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s) {
+                         int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s,
+                         const int32_t *pos, int64_t addend_rows) {
   const int64_t total = batch * positions * channels;
   if (total == 0) return 0;
   hipLaunchKernelGGL(add_requant15_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, x, tokens,
-                     addend, mult, shift, out, positions, channels, total, mpc, spc);
+                     addend, mult, shift, out, positions, channels, total, mpc, spc, pos, addend_rows);
   return check_launch("add_requant15_kernel");
 }
 
@@ -346,6 +385,16 @@ int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, in
   return check_launch("transpose_heads_kernel");
 }
 
+int launch_gather_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
+                        int64_t dst_sb, int64_t dst_sh, int64_t dst_st, int64_t t_off, int64_t B,
+                        int64_t T, int64_t H, int64_t D, hipStream_t s) {
+  const int64_t total = B * T * H * D / 16;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(gather_heads_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, src, src_sb,
+                     src_st, dst, dst_sb, dst_sh, dst_st, t_off, B, T, H, D);
+  return check_launch("gather_heads_kernel");
+}
+
 int launch_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
                      int64_t dst_sb, int64_t dst_st, int64_t t_off, int64_t B, int64_t T,
                      int64_t C, hipStream_t s) {
@@ -354,6 +403,19 @@ int launch_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *
   hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, src, src_sb,
                      src_st, dst, dst_sb, dst_st, t_off, B, T, C);
   return check_launch("copy_rows_kernel");
+}
+
+int launch_greedy_record(const int64_t *next, int64_t *history, int64_t rows, int64_t hist_ld,
+                         int64_t hist_cols, int32_t *step, int32_t *pos, int32_t pos_inc,
+                         hipStream_t s) {
+  if (rows > 0) {
+    hipLaunchKernelGGL(greedy_record_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
+                       next, history, rows, hist_ld, hist_cols, step);
+    int rc = check_launch("greedy_record_kernel");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(64), 0, s, step, pos, pos_inc);
+  return check_launch("greedy_advance_kernel");
 }
 
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,

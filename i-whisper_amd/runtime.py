@@ -167,100 +167,213 @@ class EncoderRunner:
 
 
 class DecoderRunner:
-    """Greedy TextDecoder_int steps over preallocated self/cross KV caches."""
+    """Greedy TextDecoder_int steps over preallocated self/cross KV caches.
 
-    def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int):
+    Caches are per layer and per head contiguous: self-attention K
+    [B, H, n_ctx, D] and V transposed [B, H, D, n_ctx16]; cross-attention K
+    [B, H, n_audio_ctx, D] and V transposed [B, H, D, n_audio_ctx16], projected
+    once per utterance. The prompt step runs eagerly; every later step is one
+    token per utterance and runs a fixed kernel sequence whose cache position
+    lives in device memory, so it is captured once as a HIP graph and
+    replayed (``use_graph``).
+    """
+
+    def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int,
+                 max_steps: Optional[int] = None, use_graph: bool = True):
         self.dec = decoder
         self.B = batch
         C, H = decoder.n_state, decoder.n_head
         self.C, self.H, self.D = C, H, C // H
-        self.Tmax = (decoder.n_ctx + 15) // 16 * 16
+        self.Tcap = decoder.n_ctx
+        self.tcap16 = (self.Tcap + 15) // 16 * 16
         self.Ta = n_audio_ctx
-        self.tpa = (n_audio_ctx + 15) // 16 * 16
+        self.ta16 = (n_audio_ctx + 15) // 16 * 16
+        self.use_graph = use_graph
         dev = decoder.positional_embedding.device
-        L = decoder.n_layer
+        L, D = decoder.n_layer, self.D
+        i8 = dict(dtype=torch.int8, device=dev)
         self.self_qkv = [_FusedLinear([b.attn.query, b.attn.key, b.attn.value]) for b in decoder.blocks]
         self.cross_kv = [_FusedLinear([b.cross_attn.key, b.cross_attn.value]) for b in decoder.blocks]
-        self.k_self = [torch.empty((batch, self.Tmax, C), dtype=torch.int8, device=dev) for _ in range(L)]
-        self.vt_self = [torch.empty((batch, H, self.D, self.Tmax), dtype=torch.int8, device=dev)
-                        for _ in range(L)]
-        self.kv_cross = [torch.empty((batch * n_audio_ctx, 2 * C), dtype=torch.int8, device=dev)
-                         for _ in range(L)]
-        self.vt_cross = [torch.empty((batch, H, self.D, self.tpa), dtype=torch.int8, device=dev)
-                         for _ in range(L)]
-        self.offset = 0
+        self.k_self = [torch.zeros((batch, H, self.Tcap, D), **i8) for _ in range(L)]
+        self.vt_self = [torch.zeros((batch, H, D, self.tcap16), **i8) for _ in range(L)]
+        self.k_cross = [torch.zeros((batch, H, n_audio_ctx, D), **i8) for _ in range(L)]
+        self.vt_cross = [torch.zeros((batch, H, D, self.ta16), **i8) for _ in range(L)]
+        self.kv_tmp = torch.empty((batch * n_audio_ctx, 2 * C), **i8)
+        self.self_tables = [b.attn.shift_exp_table() for b in decoder.blocks]
+        self.cross_tables = [b.cross_attn.shift_exp_table() for b in decoder.blocks]
+        # one-token step buffers
+        self.x16 = torch.empty((batch, C), dtype=torch.int16, device=dev)
+        self.h8 = torch.empty((batch, C), **i8)
+        self.q8 = torch.empty((batch, C), **i8)
+        self.wv = torch.empty((batch, C), **i8)
+        self.f8 = torch.empty((batch, 4 * C), **i8)
+        self.logits = torch.empty((batch, decoder.n_vocab), **i8)
+        # device-side decode state
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)   # tokens in the self caches
+        self.step_no = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.tokens = torch.zeros(batch, dtype=torch.int64, device=dev)
+        self.hist_cols = max_steps or decoder.n_ctx
+        self.history = torch.zeros((batch, self.hist_cols), dtype=torch.int64, device=dev)
+        self.graph = None
 
+    # ---- per utterance ----
     def set_audio(self, xa: torch.Tensor):
         """Project the cross-attention K/V of the encoder output once per utterance."""
         xa = xa.contiguous()
         B, Ta, C, H, D = self.B, self.Ta, self.C, self.H, self.D
+        kv = self.kv_tmp
         for l in range(self.dec.n_layer):
-            kv = self.kv_cross[l]
             self.cross_kv[l].linear8(xa, B * Ta, kv)
+            _lib.call("iw_gather_heads", kv.data_ptr(), Ta * 2 * C, 2 * C, self.k_cross[l].data_ptr(),
+                      H * Ta * D, Ta * D, D, 0, B, Ta, H, D, _stream())
             _lib.call("iw_transpose_heads", kv.data_ptr() + C, Ta * 2 * C, 2 * C,
-                      self.vt_cross[l].data_ptr(), H * D * self.tpa, D * self.tpa, self.tpa, 0, B, Ta,
-                      H, D, _stream())
-        self.offset = 0
+                      self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16, 0, B,
+                      Ta, H, D, _stream())
 
-    def _attend(self, att, q_ptr, q_sb, q_st, k, k_sb, k_st, vt, tp, Tq, Tk, mask, out):
+    def reset(self):
+        self.pos.zero_()
+        self.step_no.zero_()
+
+    # ---- shared pieces ----
+    def _cross_attend(self, att, l, q_ptr, q_sb, q_st, Tq, out, table):
         s = att._scalars()
-        H, D, C = self.H, self.D, self.C
-        _lib.call("iw_attention", q_ptr, q_sb, q_st, k.data_ptr(), k_sb, D, k_st, vt.data_ptr(),
-                  H * D * tp, D * tp, tp, out.data_ptr(), Tq * C, C, _ptr(mask), self.B, H, Tq, Tk,
-                  D, s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset, None, True,
-                  _stream())
+        H, D, Ta = self.H, self.D, self.Ta
+        if Tq == 1:
+            _lib.call("iw_attention_decode_cache", q_ptr, q_sb, self.k_cross[l].data_ptr(),
+                      H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
+                      D * self.ta16, self.ta16, out.data_ptr(), self.C, self.B, H, D, Ta, None, Ta,
+                      s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset, _stream())
+        else:
+            _lib.call("iw_attention", q_ptr, q_sb, q_st, self.k_cross[l].data_ptr(), H * Ta * D,
+                      Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16,
+                      self.ta16, out.data_ptr(), Tq * self.C, self.C, None, self.B, H, Tq, Ta, D,
+                      s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset,
+                      table.data_ptr(), False, _stream())
 
-    def step(self, tokens: torch.Tensor, next_out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Run the new ``tokens`` [B, T] (contiguous int64) and return the argmax of the
-        last position's int8 logits as int64 [B] (written into ``next_out`` if given)."""
+    def _finish(self, x_last: torch.Tensor, pos_inc: int):
+        """Final LayerNorm of the last position, classifier, argmax, record, advance."""
+        dec = self.dec
+        sc = dec.scalars()
+        _ln(dec.ln, x_last, self.B, self.h8)
+        _lib.call("iw_classifier", self.h8.data_ptr(), dec.token_embedding.weight.data_ptr(), sc["cm"],
+                  sc["cs"], self.logits.data_ptr(), self.B, self.C, dec.n_vocab, _stream())
+        _lib.call("iw_greedy_advance", self.logits.data_ptr(), self.B, dec.n_vocab, dec.n_vocab,
+                  self.tokens.data_ptr(), self.history.data_ptr(), self.hist_cols, self.hist_cols,
+                  self.step_no.data_ptr(), self.pos.data_ptr(), pos_inc, _stream())
+
+    # ---- the prompt (several tokens, cache empty) ----
+    def prompt_step(self, tokens: torch.Tensor):
         dec = self.dec
         B, C, H, D = self.B, self.C, self.H, self.D
-        T = tokens.shape[-1] if tokens.dim() == 2 else 1
-        off = self.offset
-        Tk = off + T
-        M = B * T
+        P = tokens.shape[1]
+        if P > self.Tcap:
+            raise ValueError("prompt longer than n_text_ctx")
+        M = B * P
         dev = tokens.device
-        x16 = dec.embed(tokens.view(B, T), off)
+        x16 = dec.embed(tokens.view(B, P), 0).view(M, C)
         h8 = torch.empty((M, C), dtype=torch.int8, device=dev)
         qkv = torch.empty((M, 3 * C), dtype=torch.int8, device=dev)
         wv = torch.empty((M, C), dtype=torch.int8, device=dev)
         qc = torch.empty((M, C), dtype=torch.int8, device=dev)
         f8 = torch.empty((M, 4 * C), dtype=torch.int8, device=dev)
-        mask = dec.mask[off:off + T, :Tk].contiguous() if T > 1 else None
+        mask = dec.mask[:P, :P].contiguous()
         for l, blk in enumerate(dec.blocks):
             sc = blk._scalars()
             _ln(blk.attn_ln, x16, M, h8)
             self.self_qkv[l].linear8(h8, M, qkv)
             q = qkv.data_ptr()
-            _lib.call("iw_copy_rows", q + C, T * 3 * C, 3 * C, self.k_self[l].data_ptr(),
-                      self.Tmax * C, C, off, B, T, C, _stream())
-            _lib.call("iw_transpose_heads", q + 2 * C, T * 3 * C, 3 * C, self.vt_self[l].data_ptr(),
-                      H * D * self.Tmax, D * self.Tmax, self.Tmax, off, B, T, H, D, _stream())
-            self._attend(blk.attn, q, T * 3 * C, 3 * C, self.k_self[l], self.Tmax * C, C,
-                         self.vt_self[l], self.Tmax, T, Tk, mask, wv)
+            _lib.call("iw_gather_heads", q + C, P * 3 * C, 3 * C, self.k_self[l].data_ptr(),
+                      H * self.Tcap * D, self.Tcap * D, D, 0, B, P, H, D, _stream())
+            _lib.call("iw_transpose_heads", q + 2 * C, P * 3 * C, 3 * C, self.vt_self[l].data_ptr(),
+                      H * D * self.tcap16, D * self.tcap16, self.tcap16, 0, B, P, H, D, _stream())
+            s = blk.attn._scalars()
+            _lib.call("iw_attention", q, P * 3 * C, 3 * C, self.k_self[l].data_ptr(), H * self.Tcap * D,
+                      self.Tcap * D, D, self.vt_self[l].data_ptr(), H * D * self.tcap16,
+                      D * self.tcap16, self.tcap16, wv.data_ptr(), P * C, C, mask.data_ptr(), B, H, P,
+                      P, D, s["qm"], s["qs"], s["f"], s["am"], s["as_"], blk.attn.rsqrt_offset,
+                      self.self_tables[l].data_ptr(), False, _stream())
             _lin32_res(blk.attn.out, wv.data_ptr(), M, x16, sc["a"])
             _ln(blk.cross_attn_ln, x16, M, h8)
             _lin8(blk.cross_attn.query, h8.data_ptr(), M, qc)
-            self._attend(blk.cross_attn, qc.data_ptr(), T * C, C, self.kv_cross[l], self.Ta * 2 * C,
-                         2 * C, self.vt_cross[l], self.tpa, T, self.Ta, None, wv)
+            self._cross_attend(blk.cross_attn, l, qc.data_ptr(), P * C, C, P, wv, self.cross_tables[l])
             _lin32_res(blk.cross_attn.out, wv.data_ptr(), M, x16, sc["c"])
             _ln(blk.mlp_ln, x16, M, h8)
             _mlp_gelu(blk, h8.data_ptr(), M, f8)
             _lin32_res(blk.mlp[2], f8.data_ptr(), M, x16, sc["m"])
-        last = x16.view(B, T, C)[:, T - 1].contiguous()
-        hl = torch.empty((B, C), dtype=torch.int8, device=dev)
-        _ln(dec.ln, last, B, hl)
-        sc = dec.scalars()
-        logits = torch.empty((B, dec.n_vocab), dtype=torch.int8, device=dev)
-        _lib.call("iw_classifier", hl.data_ptr(), dec.token_embedding.weight.data_ptr(), sc["cm"],
-                  sc["cs"], logits.data_ptr(), B, C, dec.n_vocab, _stream())
-        self.last_logits = logits
-        if next_out is None:
-            next_out = torch.empty(B, dtype=torch.int64, device=dev)
-        _lib.call("iw_argmax_rows", logits.data_ptr(), B, dec.n_vocab, dec.n_vocab, next_out.data_ptr(),
-                  _stream())
-        self.offset = Tk
-        return next_out
+        last = x16.view(B, P, C)[:, P - 1].contiguous()
+        self._finish(last, P)
+
+    # ---- one token per utterance (graph-capturable) ----
+    def decode_step(self):
+        dec = self.dec
+        B, C, H, D = self.B, self.C, self.H, self.D
+        sc0 = dec.scalars()
+        _lib.call("iw_embed_tokens", self.tokens.data_ptr(), dec.token_embedding.weight.data_ptr(),
+                  dec.positional_embedding.data_ptr(), dec.n_ctx, self.pos.data_ptr(),
+                  sc0["m16"].data_ptr(), sc0["s"].data_ptr(), self.x16.data_ptr(), B, C, _stream())
+        x16, h8, q8, wv, f8 = self.x16, self.h8, self.q8, self.wv, self.f8
+        for l, blk in enumerate(dec.blocks):
+            sc = blk._scalars()
+            fq = self.self_qkv[l]
+            _ln(blk.attn_ln, x16, B, h8)
+            _lib.call("iw_linear8_qkv_cache", h8.data_ptr(), fq.weight.data_ptr(), fq.bias.data_ptr(),
+                      fq.wz.data_ptr(), fq.mult.data_ptr(), fq.shift.data_ptr(), B, C, True, True,
+                      q8.data_ptr(), C, self.k_self[l].data_ptr(), H * self.Tcap * D, self.Tcap * D, D,
+                      self.vt_self[l].data_ptr(), H * D * self.tcap16, D * self.tcap16, self.tcap16, C,
+                      D, 1, self.Tcap, self.pos.data_ptr(), _stream())
+            s = blk.attn._scalars()
+            _lib.call("iw_attention_decode_cache", q8.data_ptr(), C, self.k_self[l].data_ptr(),
+                      H * self.Tcap * D, self.Tcap * D, D, self.vt_self[l].data_ptr(),
+                      H * D * self.tcap16, D * self.tcap16, self.tcap16, wv.data_ptr(), C, B, H, D, 1,
+                      self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
+                      blk.attn.rsqrt_offset, _stream())
+            _lin32_res(blk.attn.out, wv.data_ptr(), B, x16, sc["a"])
+            _ln(blk.cross_attn_ln, x16, B, h8)
+            _lin8(blk.cross_attn.query, h8.data_ptr(), B, q8)
+            self._cross_attend(blk.cross_attn, l, q8.data_ptr(), C, C, 1, wv, None)
+            _lin32_res(blk.cross_attn.out, wv.data_ptr(), B, x16, sc["c"])
+            _ln(blk.mlp_ln, x16, B, h8)
+            _mlp_gelu(blk, h8.data_ptr(), B, f8)
+            _lin32_res(blk.mlp[2], f8.data_ptr(), B, x16, sc["m"])
+        self._finish(x16, 1)
+
+    def _replay(self, n: int):
+        if n <= 0:
+            return
+        if not self.use_graph:
+            for _ in range(n):
+                self.decode_step()
+            return
+        if self.graph is None:
+            # one eager step loads every kernel before capture
+            self.decode_step()
+            n -= 1
+            torch.cuda.current_stream().synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.decode_step()
+            self.graph = g
+        for _ in range(n):
+            self.graph.replay()
+
+    def run(self, prompt: torch.Tensor, steps: int, keep_logits: bool = False):
+        """Greedy tokens [B, steps] after ``prompt`` (and the int8 logits of every step)."""
+        if steps > self.hist_cols:
+            raise ValueError("more steps than the history holds")
+        self.reset()
+        logits = []
+        self.prompt_step(prompt.contiguous())
+        if keep_logits:
+            logits.append(self.logits.clone())
+            for _ in range(steps - 1):
+                self.decode_step()
+                logits.append(self.logits.clone())
+        else:
+            self._replay(steps - 1)
+        toks = self.history[:, :steps]
+        if keep_logits:
+            return toks, torch.stack(logits, 1)
+        return toks
 
 
 def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torch.Tensor,
@@ -274,19 +387,13 @@ def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torc
         raise ValueError(f"prompt + steps exceeds n_text_ctx ({dec.n_ctx})")
     if int(prompt.min()) < 0 or int(prompt.max()) >= dec.n_vocab:
         raise ValueError("prompt token id out of range")
+    if steps <= 0:
+        return prompt.clone()
     if runner is None:
-        runner = DecoderRunner(dec, B, audio_features.shape[1])
+        runner = DecoderRunner(dec, B, audio_features.shape[1], use_graph=not keep_logits)
     runner.set_audio(audio_features)
-    out = torch.empty((P + steps, B), dtype=torch.int64, device=prompt.device)
-    out[:P] = prompt.t()
-    logits: List[torch.Tensor] = []
-    cur = prompt.contiguous()
-    for i in range(steps):
-        runner.step(cur, out[P + i])
-        if keep_logits:
-            logits.append(runner.last_logits.clone())
-        cur = out[P + i]
-    toks = out.t().contiguous()
+    res = runner.run(prompt, steps, keep_logits=keep_logits)
     if keep_logits:
-        return toks, torch.stack(logits, 1)
-    return toks
+        toks, logits = res
+        return torch.cat([prompt, toks], 1), logits
+    return torch.cat([prompt, res], 1)

@@ -1,0 +1,206 @@
+"""Bit-exact parity of the decode-step entry points (KV-cache layouts, device-side
+cache position, graph replay) against the CPU oracle.
+
+* iw_attention_decode_cache: one query row per (batch, head) over per-head
+  caches with garbage past the valid keys; the key count is k_length + *pos,
+  clamped to max_keys.
+* iw_linear8_qkv_cache: the QKV projection appending K / V at *pos.
+* iw_embed_tokens / iw_greedy_advance: the embedding and greedy bookkeeping
+  of a step whose position lives on the device.
+* A captured decode step replayed many times gives the eager tokens.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests import gen
+
+pytestmark = pytest.mark.gpu
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _decode_cache(iw, q, k, v, qm, qs, f, am, as_, *, tcap, k_length, pos_val, max_keys):
+    """q [B,H,1,D], k [B,H,Tk,D], v [B,H,D,Tk] placed in caches with random fill."""
+    B, H, _, D = q.shape
+    Tk = k.shape[2]
+    r = gen.rng(B + H + Tk)
+    tc16 = (tcap + 15) // 16 * 16
+    kc = gen.i8(r, (B, H, tcap, D))
+    kc[:, :, :Tk] = k
+    vc = gen.i8(r, (B, H, D, tc16))
+    vc[..., :Tk] = v
+    qh = np.ascontiguousarray(q[:, :, 0, :].reshape(B, H * D))
+    out = torch.empty((B, H * D), dtype=torch.int8, device="cuda")
+    pos = None if pos_val is None else torch.tensor([pos_val], dtype=torch.int32, device="cuda")
+    qt, kt, vt = T(qh), T(kc), T(vc)
+    iw._lib.call("iw_attention_decode_cache", qt.data_ptr(), H * D, kt.data_ptr(), H * tcap * D,
+                 tcap * D, D, vt.data_ptr(), H * D * tc16, D * tc16, tc16, out.data_ptr(), H * D, B, H,
+                 D, k_length, None if pos is None else pos.data_ptr(), max_keys, qm, qs, f, am, as_, 16,
+                 stream())
+    return host(out).reshape(B, 1, H * D)
+
+
+@pytest.mark.parametrize("B,H,D,Tk,tcap,k_length", [
+    (2, 3, 64, 1, 448, 1), (2, 3, 64, 17, 448, 1), (1, 2, 64, 448, 448, 1), (3, 2, 64, 200, 448, 1),
+    (2, 4, 64, 1500, 1500, 1500), (1, 2, 96, 100, 448, 1), (1, 1, 128, 300, 448, 1),
+    (2, 2, 64, 33, 40, 33)])
+def test_attention_decode_cache(iw, oracle, gpu, B, H, D, Tk, tcap, k_length):
+    print("case: decode cache", B, H, D, Tk, tcap, k_length, flush=True)
+    q, k, v, qm, qs, f, am, as_ = gen.attn_case(3 * B + Tk + D, B, H, 1, Tk, D)
+    exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
+    pos_val = None if k_length == Tk else Tk - k_length
+    got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=k_length,
+                        pos_val=pos_val, max_keys=tcap if pos_val is not None else k_length)
+    assert np.array_equal(got, exp)
+
+
+def test_attention_decode_cache_clamps_keys(iw, oracle, gpu):
+    """A device position past the cache reads max_keys keys, not beyond."""
+    B, H, D, tcap = 1, 2, 64, 64
+    q, k, v, qm, qs, f, am, as_ = gen.attn_case(77, B, H, 1, tcap, D)
+    exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
+    got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=1, pos_val=10_000,
+                        max_keys=tcap)
+    assert np.array_equal(got, exp)
+
+
+def test_attention_decode_cache_wrap_corner(iw, oracle, gpu):
+    B, H, D, Tk = 1, 1, 64, 40
+    q = np.full((B, H, 1, D), 127, np.int8)
+    k = np.full((B, H, Tk, D), 127, np.int8)
+    k[..., 1::3, :] = -128
+    v = gen.i8(gen.rng(1), (B, H, D, Tk))
+    exp = oracle.attention(q, k, v, None, 255, 0, 8, 200, 6)
+    got = _decode_cache(iw, q, k, v, 255, 0, 8, 200, 6, tcap=448, k_length=1, pos_val=Tk - 1,
+                        max_keys=448)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("B,Tn,H,D,pos_val,tcap", [(1, 1, 2, 64, 0, 448), (5, 1, 2, 64, 7, 448),
+                                                    (128, 1, 2, 64, 100, 448), (4, 3, 2, 64, 0, 448),
+                                                    (2, 3, 4, 32, 38, 40), (40, 3, 2, 64, 5, 448)])
+def test_linear8_qkv_cache(iw, oracle, gpu, B, Tn, H, D, pos_val, tcap):
+    print("case: qkv cache", B, Tn, H, D, pos_val, tcap, flush=True)
+    C = H * D
+    M = B * Tn
+    x, w, b, z, m, s = gen.realistic_linear_case(M + C + pos_val, M, C, 3 * C)
+    exp = oracle.linear8(x, w, b, z, m, s)
+    r = gen.rng(5)
+    tc16 = (tcap + 15) // 16 * 16
+    kc0 = gen.i8(r, (B, H, tcap, D))
+    vc0 = gen.i8(r, (B, H, D, tc16))
+    kc, vc = T(kc0), T(vc0)
+    q = torch.empty((M, C), dtype=torch.int8, device="cuda")
+    pos = torch.tensor([pos_val], dtype=torch.int32, device="cuda")
+    xt, wt, bt, zt, mt, st = T(x), T(w), T(b), T(z), T(m), T(s)  # alive across the call
+    iw._lib.call("iw_linear8_qkv_cache", xt.data_ptr(), wt.data_ptr(), bt.data_ptr(), zt.data_ptr(),
+                 mt.data_ptr(), st.data_ptr(), M, C, True, True, q.data_ptr(), C,
+                 kc.data_ptr(), H * tcap * D, tcap * D, D, vc.data_ptr(), H * D * tc16, D * tc16, tc16,
+                 C, D, Tn, tcap, pos.data_ptr(), stream())
+    torch.cuda.synchronize()
+    assert np.array_equal(host(q), exp[:, :C])
+    kexp, vexp = kc0.copy(), vc0.copy()
+    e = exp.reshape(B, Tn, 3, H, D)
+    for i in range(Tn):
+        t = pos_val + i
+        if t < tcap:
+            kexp[:, :, t, :] = e[:, i, 1]
+            vexp[:, :, :, t] = e[:, i, 2]
+    assert np.array_equal(host(kc), kexp)
+    assert np.array_equal(host(vc), vexp)
+
+
+def test_embed_tokens(iw, oracle, gpu):
+    r = gen.rng(11)
+    B, V, C, n_ctx = 6, 500, 128, 40
+    table = gen.i8(r, (V, C))
+    pe = gen.i8(r, (n_ctx, C))
+    tokens = r.integers(0, V, size=B).astype(np.int64)
+    m16 = np.array([int(r.integers(1, 65536))], np.uint16)
+    s8 = np.array([9], np.int8)
+    tt, tab, pet, mt, st = T(tokens), T(table), T(pe), T(m16), T(s8)  # alive across the calls
+    for pos_val in (0, 17, n_ctx - 1, n_ctx + 5):
+        pos = torch.tensor([pos_val], dtype=torch.int32, device="cuda")
+        out = torch.empty((B, C), dtype=torch.int16, device="cuda")
+        iw._lib.call("iw_embed_tokens", tt.data_ptr(), tab.data_ptr(), pet.data_ptr(), n_ctx,
+                     pos.data_ptr(), mt.data_ptr(), st.data_ptr(), out.data_ptr(), B, C, stream())
+        p = min(pos_val, n_ctx - 1)  # a position past the table reads its last row
+        exp = oracle.add_requant15(table[tokens][:, None, :], pe[p:p + 1], m16, s8)
+        assert np.array_equal(host(out), exp[:, 0])
+
+
+def test_greedy_advance(iw, gpu):
+    r = gen.rng(12)
+    B, V, cols = 5, 1000, 4
+    hist = torch.full((B, cols), -1, dtype=torch.int64, device="cuda")
+    nxt = torch.empty(B, dtype=torch.int64, device="cuda")
+    step = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = torch.tensor([3], dtype=torch.int32, device="cuda")
+    rows = []
+    for i in range(cols + 1):
+        lg = gen.i8(r, (B, V))
+        lg[0, 10] = lg[0, 20] = 127  # first maximum wins
+        lgt = T(lg)
+        iw._lib.call("iw_greedy_advance", lgt.data_ptr(), B, V, V, nxt.data_ptr(), hist.data_ptr(),
+                     cols, cols, step.data_ptr(), pos.data_ptr(), 1 if i else 3, stream())
+        assert np.array_equal(host(nxt), np.argmax(lg, 1))
+        rows.append(np.argmax(lg, 1))
+    assert np.array_equal(host(hist), np.stack(rows[:cols], 1))  # the extra step is not recorded
+    assert int(step.item()) == cols + 1 and int(pos.item()) == 3 + 3 + cols
+
+
+def test_gather_heads(iw, gpu):
+    r = gen.rng(13)
+    B, Tn, H, D, tcap, off = 3, 7, 4, 32, 20, 5
+    src = gen.i8(r, (B, Tn, 3, H * D))
+    dst0 = gen.i8(r, (B, H, tcap, D))
+    dst = T(dst0)
+    st = T(src)
+    iw._lib.call("iw_gather_heads", st.data_ptr() + H * D, Tn * 3 * H * D, 3 * H * D, dst.data_ptr(),
+                 H * tcap * D, tcap * D, D, off, B, Tn, H, D, stream())
+    exp = dst0.copy()
+    exp[:, :, off:off + Tn, :] = src[:, :, 1].reshape(B, Tn, H, D).transpose(0, 2, 1, 3)
+    assert np.array_equal(host(dst), exp)
+
+
+@pytest.fixture(scope="module")
+def tiny_model(iw):
+    dims = iw.ModelDimensions(n_mels=80, n_audio_ctx=50, n_audio_state=384, n_audio_head=6,
+                              n_audio_layer=1, n_vocab=300, n_text_ctx=24, n_text_state=384,
+                              n_text_head=6, n_text_layer=2)
+    params = iw.synth.calibrated_int_params(dims, seed=99, calib_ctx=50)
+    return dims, params
+
+
+def test_graph_replay_matches_eager_and_oracle(iw, gpu, tiny_model):
+    """The captured one-token step, replayed across two utterances, gives the eager
+    tokens and the oracle's."""
+    from oracle.model_oracle import OracleWhisper
+
+    dims, params = tiny_model
+    model = iw.Whisper_int.from_params(dims, params).cuda()
+    ref = OracleWhisper(dims, params, threads=4)
+    B, steps = 3, 12
+    runner = iw.DecoderRunner(model.decoder, B, dims.n_audio_ctx, use_graph=True)
+    for seed in (1, 2):
+        mel = iw.synth.synthetic_mel(B, dims.n_mels, 2 * dims.n_audio_ctx, seed=seed)
+        prompt = np.random.default_rng(seed).integers(0, dims.n_vocab, size=(B, 3)).astype(np.int64)
+        with torch.no_grad():
+            feats = model.embed_audio(T(mel))
+            g_toks = iw.greedy_decode(model, feats, T(prompt), steps, runner=runner)
+            e_toks, _ = iw.greedy_decode(model, feats, T(prompt), steps, keep_logits=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(g_toks), host(e_toks)), f"utterance {seed}"
+        r_toks = ref.greedy(ref.encoder(mel), prompt, steps)
+        assert np.array_equal(host(g_toks), r_toks), f"utterance {seed}"
