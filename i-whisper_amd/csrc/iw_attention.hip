@@ -457,12 +457,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
 //      row; the per-lane partial sums are reduced once per row.
 constexpr int DC_MAX_TK = 4096;
 
-template <int D>
+template <int D, int PRE>
 __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, const int32_t *pos) {
   constexpr int CPK = D / 16;                      // 16-byte chunks per key
   constexpr int LPK = CPK <= 4 ? 4 : 8;            // lanes per key
   constexpr int KPW = 64 / LPK;                    // keys per wave load
   constexpr int RPW = D / 4;                       // V^T rows per wave
+  constexpr int UK = 4;                            // key loads in flight per lane
   __shared__ int32_t sS[DC_MAX_TK];
   __shared__ __attribute__((aligned(16))) uint8_t sP[DC_MAX_TK];
   __shared__ int32_t sRed[4];
@@ -474,7 +475,22 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
   const int h = (int)(bh % a.H);
   const int64_t b = bh / a.H;
   const int Tk = min(a.Tk + (pos ? *pos : 0), a.max_tk);
+  const int tk16 = (Tk + 15) & ~15;
+  const int nch = tk16 >> 4;
   if (tid == 0) sHi = 0;
+
+  // V^T rows of this wave: the first PRE chunk sets (chunks lane + 64 i) are
+  // requested now, so they stream in while the scores are computed
+  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)(wave * RPW) * a.v_sd;
+  uint4 vpre[PRE][RPW];
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) {
+    const int c = lane + 64 * i;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      vpre[i][r] = c < nch ? *reinterpret_cast<const uint4 *>(vb + (int64_t)r * a.v_sd + c * 16)
+                           : make_uint4(0, 0, 0, 0);
+  }
 
   // ---- phase 1: raw scores ----
   const int chunk = lane % LPK;
@@ -484,21 +500,29 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
     qv = *reinterpret_cast<const v4i *>(a.q + b * a.q_sb + (int64_t)h * D + chunk * 16);
   const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh;
   int32_t mx = INT32_MIN;
-  for (int j0 = wave * KPW; j0 < Tk; j0 += 4 * KPW) {
-    const int j = j0 + lane / LPK;
-    int32_t acc = 0;
-    if (j < Tk && cvalid) {
-      const v4i kv = *reinterpret_cast<const v4i *>(kb + (int64_t)j * a.k_st + chunk * 16);
-      acc = __builtin_amdgcn_sdot4(qv[0], kv[0], acc, false);
-      acc = __builtin_amdgcn_sdot4(qv[1], kv[1], acc, false);
-      acc = __builtin_amdgcn_sdot4(qv[2], kv[2], acc, false);
-      acc = __builtin_amdgcn_sdot4(qv[3], kv[3], acc, false);
+  for (int j0 = wave * KPW; j0 < Tk; j0 += 4 * KPW * UK) {
+    v4i kv[UK];
+#pragma unroll
+    for (int u = 0; u < UK; ++u) {
+      const int j = j0 + u * 4 * KPW + lane / LPK;
+      kv[u] = (j < Tk && cvalid)
+                  ? *reinterpret_cast<const v4i *>(kb + (int64_t)j * a.k_st + chunk * 16)
+                  : v4i{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int o = 1; o < LPK; o <<= 1) acc += __shfl_xor(acc, o);
-    if (j < Tk) {
-      if (chunk == 0) sS[j] = acc;
-      mx = max(mx, acc);
+    for (int u = 0; u < UK; ++u) {
+      const int j = j0 + u * 4 * KPW + lane / LPK;
+      int32_t acc = 0;
+      acc = __builtin_amdgcn_sdot4(qv[0], kv[u][0], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[1], kv[u][1], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[2], kv[u][2], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[3], kv[u][3], acc, false);
+#pragma unroll
+      for (int o = 1; o < LPK; o <<= 1) acc += __shfl_xor(acc, o);
+      if (j < Tk) {
+        if (chunk == 0) sS[j] = acc;
+        mx = max(mx, acc);
+      }
     }
   }
 #pragma unroll
@@ -510,7 +534,6 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
   const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
 
   // ---- phase 2: P and its row sum ----
-  const int tk16 = (Tk + 15) & ~15;
   uint32_t psum = 0, hi = 0;
   for (int j = tid; j < tk16; j += 256) {
     uint32_t p = 0;
@@ -533,18 +556,14 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
   const bool any_hi = sHi != 0;
 
   // ---- phase 3: O = P . V^T ----
-  const int nch = tk16 >> 4;
-  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)(wave * RPW) * a.v_sd;
   uint32_t accd[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) accd[r] = 0;
-  for (int c = lane; c < nch; c += 64) {
-    const uint4 pv = reinterpret_cast<const uint4 *>(sP)[c];
+  auto consume = [&](const uint4 pv, const uint4 *vv) {
     const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      const uint4 vv = *reinterpret_cast<const uint4 *>(vb + (int64_t)r * a.v_sd + c * 16);
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+      const uint32_t vw[4] = {vv[r].x, vv[r].y, vv[r].z, vv[r].w};
       if (!any_hi) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -561,6 +580,17 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
         accd[r] += (uint32_t)hs << 7;
       }
     }
+  };
+#pragma unroll
+  for (int i = 0; i < PRE; ++i) {
+    const int c = lane + 64 * i;
+    if (c < nch) consume(reinterpret_cast<const uint4 *>(sP)[c], vpre[i]);
+  }
+  for (int c = lane + 64 * PRE; c < nch; c += 64) {
+    uint4 vv[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) vv[r] = *reinterpret_cast<const uint4 *>(vb + (int64_t)r * a.v_sd + c * 16);
+    consume(reinterpret_cast<const uint4 *>(sP)[c], vv);
   }
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
@@ -581,6 +611,189 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
     a.out[b * a.o_sb + (int64_t)h * D + d] = (int8_t)clampi(y, -127, 127);
   }
 }
+
+// ---------------------------------------------------------------------------
+// Decode attention over the caches for head_dim 64 (every Whisper size),
+// streaming K and V through LDS.
+//
+// One block per (batch, head) reads Tk x 64 bytes of K and 64 x Tk bytes of
+// V^T, nothing else of size, so the kernel is HBM-bound and a CU needs many
+// bytes in flight (bandwidth x latency). Both operands flow through one ring
+// of NR 4 KB slots in 64-key chunks: K chunks 0 .. nK-1, then V^T chunks, so
+// the copies of V are already under way while the row maximum and P are
+// formed. Each chunk is one global_load_lds_dwordx4 per wave, and every lane
+// later reads back exactly the 16 bytes it copied (K: key w*16 + l/4, bytes
+// 16 (l%4); V^T: row d = w*16 + l/4, keys 16 (l%4) of the chunk), so a wave
+// only waits for its own copies (vmcnt) and the ring needs no barrier.
+// Keys past Tk read the last valid key / chunk; their scores are dropped and
+// their P is 0.
+// ---------------------------------------------------------------------------
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(n) for a run-time n in [0, N]
+template <int N>
+__device__ __forceinline__ void wait_vm_upto(int n) {
+  if (n >= N) {
+    wait_vm<N>();
+  } else if constexpr (N > 0) {
+    wait_vm_upto<N - 1>(n);
+  }
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// global_load_lds_dwordx4: lane l copies 16 bytes from src to LDS byte
+// address lds + 16 l. Inline assembly, so that the compiler adds no waits.
+__device__ __forceinline__ void dma16_lds(const int8_t *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// the LDS part of a barrier: this wave's LDS writes are done, then all waves
+// meet (without __syncthreads' release fence, which would drain the copies)
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int MAXK, int NR>
+__global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
+  constexpr int D = 64, CH = 64;
+  __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * 4096];
+  __shared__ int16_t sS[MAXK];  // requantized scores
+  __shared__ __attribute__((aligned(16))) uint8_t sP[MAXK];
+  __shared__ int32_t sRed[4];
+  __shared__ uint32_t sSum[4];
+  __shared__ uint32_t sHi;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t bh = blockIdx.x;
+  const int h = (int)(bh % a.H);
+  const int64_t b = bh / a.H;
+  const int Tk = min(a.Tk + (pos ? *pos : 0), a.max_tk);
+  const int nK = (Tk + CH - 1) / CH;  // chunks per operand
+  const int T = 2 * nK;
+  if (tid == 0) sHi = 0;
+
+  const int kl = wave * 16 + (lane >> 2);  // key (K) or d-row (V^T) within a chunk
+  const int cq = lane & 3;                 // 16-byte piece
+  const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh + cq * 16;
+  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)kl * a.v_sd;
+  const int vlast = Tk > 0 ? ((Tk - 1) & ~15) : 0;  // last V^T piece holding a valid key
+  const uint32_t ring =
+      __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sRing)) + wave * 1024;
+  auto issue = [&](int i) {
+    const uint32_t dst = ring + (i % NR) * 4096;
+    if (i < nK) {
+      const int j = min(i * CH + kl, Tk - 1);
+      dma16_lds(kb + (int64_t)j * a.k_st, dst);
+    } else {
+      dma16_lds(vb + min((i - nK) * CH + cq * 16, vlast), dst);
+    }
+  };
+
+  // q: lane l needs bytes 16 (l % 4) of the head's 64. It is copied first,
+  // into the last ring slot (free until chunk NR - 1), so the chunk waits
+  // cover it.
+  dma16_lds(a.q + b * a.q_sb + (int64_t)h * D + cq * 16, ring + (NR - 1) * 4096);
+#pragma unroll
+  for (int i = 0; i < NR - 1; ++i)
+    if (i < T) issue(i);
+
+  int32_t mx = -32768;
+  uint32_t accd = 0;
+  int32_t hs = 0;
+  int32_t inv = 0;
+  bool any_hi = false;
+  v4i qv = v4i{0, 0, 0, 0};
+
+  // row maximum, P and its sum once every score is in sS
+  auto form_p = [&]() {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+    if (lane == 0) sRed[wave] = mx;
+    lds_barrier();
+    const int32_t rowmax = max(max(sRed[0], sRed[1]), max(sRed[2], sRed[3]));
+    const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
+    uint32_t psum = 0, hi = 0;
+    for (int j = tid; j < nK * CH; j += 256) {
+      uint32_t p = 0;
+      // x_sub = qk - rmp1 modulo 2^16
+      if (j < Tk) p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)sS[j] - rmp1), a.frac_bits);
+      sP[j] = (uint8_t)p;
+      psum += p;
+      hi |= p;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) psum += (uint32_t)__shfl_xor((int)psum, off);
+    if (lane == 0) sSum[wave] = psum;
+    if (hi & 0x80u) atomicOr(&sHi, 1u);
+    lds_barrier();
+    inv = fisr((int32_t)(sSum[0] + sSum[1] + sSum[2] + sSum[3]), a.rsqrt_off);
+    any_hi = sHi != 0;
+  };
+
+  if (nK == 0) {
+    wait_vm<0>();
+    form_p();
+  }
+  for (int i = 0; i < T; ++i) {
+    wait_vm_upto<NR - 2>(min(NR - 2, T - 1 - i));
+    if (i == 0) {
+      qv = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * 4096 + wave * 1024 + lane * 16);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // q is read before its slot refills
+    }
+    const v4i x = *reinterpret_cast<const v4i *>(sRing + (i % NR) * 4096 + wave * 1024 + lane * 16);
+    // the slot of chunk i - 1 is free: this wave read it last iteration
+    if (i + NR - 1 < T) issue(i + NR - 1);
+    if (i < nK) {
+      int32_t acc = __builtin_amdgcn_sdot4(qv[0], x[0], 0, false);
+      acc = __builtin_amdgcn_sdot4(qv[1], x[1], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[2], x[2], acc, false);
+      acc = __builtin_amdgcn_sdot4(qv[3], x[3], acc, false);
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      const int j = i * CH + kl;
+      if (j < Tk) {
+        const int32_t h16 = qk_requant16(acc, a.qk_m, a.qk_s);
+        if (cq == 0) sS[j] = (int16_t)h16;
+        mx = max(mx, h16);
+      }
+      if (i == nK - 1) form_p();
+    } else {
+      const uint4 pv = *reinterpret_cast<const uint4 *>(sP + (i - nK) * CH + cq * 16);
+      const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
+      if (!any_hi) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accd = (uint32_t)__builtin_amdgcn_sdot4((int)pw[e], x[e], (int)accd, false);
+      } else {
+        // P = 128 only after an int16 row-max wrap: split off the top bit
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          accd = (uint32_t)__builtin_amdgcn_sdot4((int)(pw[e] & 0x7f7f7f7fu), x[e], (int)accd, false);
+          hs = __builtin_amdgcn_sdot4((int)((pw[e] >> 7) & 0x01010101u), x[e], hs, false);
+        }
+      }
+    }
+  }
+  accd += (uint32_t)hs << 7;
+  accd += (uint32_t)__shfl_xor((int)accd, 1);
+  accd += (uint32_t)__shfl_xor((int)accd, 2);
+  if (cq == 0) {
+    int32_t y = rshift((int32_t)(accd * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+    a.out[b * a.o_sb + (int64_t)h * D + kl] = (int8_t)clampi(y, -127, 127);
+  }
+}
+
 }  // namespace
 
 int launch_qk_requant_rowmax(const int8_t *q, const int8_t *k, const uint8_t *mask, int16_t *qk,
@@ -644,22 +857,37 @@ int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s) {
 
 int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s) {
   if ((int64_t)a.B * a.H == 0) return 0;
+  // a set is one 16-key chunk of V^T per lane, 1024 keys per wave; up to two
+  // sets are loaded into registers before the scores are computed
+  const int sets = ((a.max_tk + 15) / 16 + 63) / 64;
+  const dim3 grid((unsigned)(a.B * a.H));
+  // head_dim 64 with 16-byte key rows and V^T rows: the streaming kernel
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.vt) |
+                       reinterpret_cast<uintptr_t>(a.q) | (uintptr_t)a.k_st | (uintptr_t)a.k_sh |
+                       (uintptr_t)a.k_sb | (uintptr_t)a.v_sd | (uintptr_t)a.v_sh | (uintptr_t)a.v_sb |
+                       (uintptr_t)a.q_sb;
+  if (a.D == 64 && (al & 15) == 0 && a.max_tk <= DC_MAX_TK) {
+    if (a.max_tk <= 2048)
+      hipLaunchKernelGGL((attn_decode_stream_kernel<2048, 8>), grid, dim3(256), 0, s, a, pos);
+    else
+      hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, 8>), grid, dim3(256), 0, s, a, pos);
+    return check_launch("attn_decode_stream_kernel");
+  }
+#define IW_DC(D_, P_) hipLaunchKernelGGL((attn_decode_cache_kernel<D_, P_>), grid, dim3(256), 0, s, a, pos)
   switch (a.D) {
     case 64:
-      hipLaunchKernelGGL(attn_decode_cache_kernel<64>, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a,
-                         pos);
+      if (sets <= 1) IW_DC(64, 1); else IW_DC(64, 2);
       break;
     case 96:
-      hipLaunchKernelGGL(attn_decode_cache_kernel<96>, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a,
-                         pos);
+      IW_DC(96, 1);
       break;
     case 128:
-      hipLaunchKernelGGL(attn_decode_cache_kernel<128>, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s,
-                         a, pos);
+      IW_DC(128, 1);
       break;
     default:
       return fail("decode attention supports head_dim 64, 96 and 128");
   }
+#undef IW_DC
   return check_launch("attn_decode_cache_kernel");
 }
 

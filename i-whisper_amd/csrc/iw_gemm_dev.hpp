@@ -141,13 +141,42 @@ struct ColParams {
   Shift pe_s;
 };
 
+// The per-column parameter values as stored, before decoding: a kernel can
+// request them early and decode them (decode_col) after its main loop, so
+// that no wait for them lands in between.
+struct ColRaw {
+  int32_t wz, bias, s, is, os, ps;
+  uint32_t m, im, om, pm;
+};
+
+// Fields whose pointer is null stay unset here and are never read by
+// decode_col, so no select consumes a loaded value before it is needed.
+__device__ __forceinline__ ColRaw load_col_raw(const GemmArgs &g, int64_t n) {
+  ColRaw r;
+  if (g.wz) r.wz = g.wz[n];
+  if (g.bias) r.bias = g.bias[n];
+  if (g.mult) r.m = g.mult[g.mult_pc ? n : 0];
+  if (g.shift) r.s = g.shift[g.mult_pc ? n : 0];
+  if (g.lut) {
+    r.is = g.luti_s[g.luti_pc ? n : 0];
+    r.os = g.luto_s[g.luto_pc ? n : 0];
+    r.im = g.luti_m[g.luti_pc ? n : 0];
+    r.om = g.luto_m[g.luto_pc ? n : 0];
+  }
+  if (g.pe) {
+    r.pm = g.pe_mult[g.pe_mpc ? n : 0];
+    r.ps = g.pe_shift[g.pe_spc ? n : 0];
+  }
+  return r;
+}
+
 template <int EPI>
-__device__ __forceinline__ ColParams load_col(const GemmArgs &g, int64_t n) {
+__device__ __forceinline__ ColParams decode_col(const GemmArgs &g, const ColRaw &r) {
   ColParams c;
-  c.wz = g.wz ? (uint32_t)(int32_t)g.wz[n] : 0u;
-  c.bias = g.bias ? (uint32_t)g.bias[n] : 0u;
-  uint32_t m = g.mult ? g.mult[g.mult_pc ? n : 0] : g.scalar_mult;
-  int32_t s = g.shift ? g.shift[g.mult_pc ? n : 0] : g.scalar_shift;
+  c.wz = g.wz ? (uint32_t)r.wz : 0u;
+  c.bias = g.bias ? (uint32_t)r.bias : 0u;
+  uint32_t m = g.mult ? r.m : g.scalar_mult;
+  int32_t s = g.shift ? r.s : g.scalar_shift;
   if (EPI == EPI_L8) {
     // linear8_scalar.cpp:71-74: a shift outside [0, 31] gives 0
     if (s < 0 || s >= 32) m = 0, s = 0;
@@ -165,12 +194,9 @@ __device__ __forceinline__ ColParams load_col(const GemmArgs &g, int64_t n) {
   c.gi_m = c.go_m = c.pe_m = 0;
   c.gi_s = c.go_s = c.pe_s = make_shift(0);
   if (g.lut) {
-    int32_t is = g.luti_s[g.luti_pc ? n : 0];
-    int32_t os = g.luto_s[g.luto_pc ? n : 0];
-    uint32_t im = g.luti_m[g.luti_pc ? n : 0];
-    uint32_t om = g.luto_m[g.luto_pc ? n : 0];
-    is = is < 0 ? 0 : is;  // gelu_scalar.cpp: shifts clamped to [0, 32]
-    os = os < 0 ? 0 : os;
+    int32_t is = r.is < 0 ? 0 : r.is;  // gelu_scalar.cpp: shifts clamped to [0, 32]
+    int32_t os = r.os < 0 ? 0 : r.os;
+    uint32_t im = r.im, om = r.om;
     if (is >= 32) im = 0, is = 0;
     if (os >= 32) om = 0, os = 0;
     c.gi_m = im;
@@ -179,14 +205,18 @@ __device__ __forceinline__ ColParams load_col(const GemmArgs &g, int64_t n) {
     c.go_s = make_shift((uint32_t)os);
   }
   if (g.pe) {
-    uint32_t pm = g.pe_mult[g.pe_mpc ? n : 0];
-    int32_t ps = g.pe_shift[g.pe_spc ? n : 0];
-    ps = ps < 0 ? 0 : ps;
+    uint32_t pm = r.pm;
+    int32_t ps = r.ps < 0 ? 0 : r.ps;
     if (ps >= 32) pm = 0, ps = 0;
     c.pe_m = pm;
     c.pe_s = make_shift((uint32_t)ps);
   }
   return c;
+}
+
+template <int EPI>
+__device__ __forceinline__ ColParams load_col(const GemmArgs &g, int64_t n) {
+  return decode_col<EPI>(g, load_col_raw(g, n));
 }
 
 // Integer GeLU on a clamped int8 value with decoded parameters

@@ -2,14 +2,22 @@
 // Linear32 (+residual15), classifier, and the self-attention QKV projection
 // whose epilogue writes Q to a buffer and appends K and V to the KV caches.
 //
-// Decode GEMMs read every weight byte once and little else, so the kernel is
-// organised for HBM streaming, not MFMA reuse: one block of 8 waves per
-// 32-column tile of the output; wave w takes m-subtile w % MS (32 rows) and
-// the K slice w / MS of KS = 8 / MS slices, loads its 16-byte A and B
-// fragments straight from global memory (A stays in L2, B streams from HBM),
-// and runs v_mfma_i32_32x32x32_i8 on them. The slices' int32 partial sums are
-// added in LDS (exact modulo 2^32 in any order), then all 512 threads run the
-// epilogue, one column per 16 threads.
+// A decode GEMM reads every weight byte once; with M <= 128 the MFMA work is
+// small and the time goes into moving operands. Each block owns one 32-column
+// tile of the output and all of K, so it reads the whole A operand (M x K,
+// L2-resident) and its own 32 weight rows: the per-CU load path, not HBM,
+// bounds it, and what matters is how many cache lines each wave-wide load
+// touches. Two kernels:
+//
+// * gemm_skinny_lds_kernel (K % 128 == 0, 16-byte aligned rows): operands
+//   move global -> LDS with global_load_lds_dwordx4 in 128-byte K stages
+//   through a 3-stage ring; every wave-wide copy reads 8 rows x 128 bytes,
+//   i.e. 8 whole cache lines. Wave w < MS multiplies m-subtile w (32 rows)
+//   by the 32 columns over all of K, reading its v_mfma_i32_32x32x32_i8
+//   fragments from LDS, and applies the epilogue from registers.
+// * gemm_skinny_kernel (any K % 16 == 0): fragments are loaded straight from
+//   global memory into registers (32 rows x 32 bytes per wave-wide load),
+//   eight waves split M and K, and the K slices are added in LDS.
 #include "iw_gemm_dev.hpp"
 
 namespace iw {
@@ -18,8 +26,261 @@ using namespace gemm;
 
 namespace {
 
-constexpr int NT = 512;   // 8 waves
 constexpr int TN = 32;    // output columns per block
+
+// Epilogue of one output element: `a` is the accumulator after the
+// zero-point and bias terms, m / n its row and column, `res` the residual
+// input of Linear32 + residual15.
+template <int EPI, bool GELU, bool SCATTER>
+__device__ __forceinline__ void skinny_store(const GemmArgs &g, const SkinnyScatter &sc,
+                                             const ColParams &c, const uint8_t *lut, int pos, int m,
+                                             int n, uint32_t a, int32_t res) {
+  if (EPI == EPI_L8 || EPI == EPI_S8) {
+    int32_t y = clampi(apply_shift(mulh_su((int32_t)a, c.mult), c.shift), -127, 127);
+    if (GELU) y = gelu_dec(y, lut, c);
+    if (SCATTER) {
+      // columns [0, C): Q; [C, 2C): K appended at position pos + (m % T)
+      // of the [B, H, T_cache, D] cache; [2C, 3C): V appended to the
+      // transposed [B, H, D, T_cache] cache
+      const int b = m / sc.T, t = pos + m % sc.T;
+      if (n < sc.C) {
+        sc.q[(int64_t)m * sc.ldq + n] = (int8_t)y;
+      } else if (t < 0 || t >= sc.t_cap) {
+        // position outside the cache: nothing is appended
+      } else if (n < 2 * sc.C) {
+        const int h = (n - sc.C) / sc.D, d = (n - sc.C) % sc.D;
+        sc.k[(int64_t)b * sc.k_sb + (int64_t)h * sc.k_sh + (int64_t)t * sc.k_st + d] = (int8_t)y;
+      } else {
+        const int h = (n - 2 * sc.C) / sc.D, d = (n - 2 * sc.C) % sc.D;
+        sc.v[(int64_t)b * sc.v_sb + (int64_t)h * sc.v_sh + (int64_t)d * sc.v_sd + t] = (int8_t)y;
+      }
+    } else {
+      reinterpret_cast<int8_t *>(g.out)[(int64_t)m * g.ldc + n] = (int8_t)y;
+    }
+  } else {
+    const int32_t br = (int32_t)((uint32_t)mulh_su((int32_t)a, c.mult) << c.shift.sh);
+    if (EPI == EPI_L32) {
+      reinterpret_cast<int32_t *>(g.out)[(int64_t)m * g.ldc + n] = br;
+    } else {
+      const uint32_t v = (uint32_t)br + (uint32_t)(res * (int32_t)g.res_mult);
+      const int32_t y = clampi(rshift_pos((int32_t)v, 15), -16383, 16383);
+      reinterpret_cast<int16_t *>(g.out)[(int64_t)m * g.ldc + n] = (int16_t)y;
+    }
+  }
+}
+
+__device__ __forceinline__ int32_t sum16v(v4i v, int32_t acc) {
+  const int ones = 0x01010101;
+  acc = __builtin_amdgcn_sdot4(v[0], ones, acc, false);
+  acc = __builtin_amdgcn_sdot4(v[1], ones, acc, false);
+  acc = __builtin_amdgcn_sdot4(v[2], ones, acc, false);
+  return __builtin_amdgcn_sdot4(v[3], ones, acc, false);
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged kernel
+// ---------------------------------------------------------------------------
+
+constexpr int LNT = 256;   // 4 waves
+constexpr int SK = 128;    // K bytes per stage (one LDS row)
+
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): the wave
+// writes 1 KB at LDS byte address `lds` (lane l at lds + 16 l). Issued as
+// inline assembly so that the compiler adds no waits for it; the loop waits
+// on vmcnt itself. No kernel using it keeps a value in M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const int8_t *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// LDS rows are 128 bytes (8 chunks of 16); chunk c of row r sits at position
+// c ^ swz8(r). A fragment read (16 consecutive lanes = 16 consecutive rows,
+// one logical chunk) then covers every (row parity, position) pair once, so
+// the 16 lanes of each ds_read_b128 pass hit distinct banks.
+__device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
+
+// SST stages in the ring, SST - 1 of them in flight while one is consumed:
+// a CU's load rate is bytes in flight / latency, so a grid with one block per
+// CU takes a deep ring (most of the LDS) and a larger grid a shallow one that
+// lets blocks share a CU.
+template <int EPI, bool GELU, bool SCATTER, int MS, int SST>
+__global__ __launch_bounds__(LNT) void gemm_skinny_lds_kernel(GemmArgs g, SkinnyScatter sc) {
+  constexpr int A_ST = MS * 32 * SK, B_ST = TN * SK;
+  constexpr int DMA_PER_WAVE = MS + 1;  // copies one wave issues per stage
+  __shared__ __attribute__((aligned(1024))) int8_t sA[SST * A_ST];
+  __shared__ __attribute__((aligned(1024))) int8_t sB[SST * B_ST];
+  __shared__ int32_t sXs[MS * 32];
+  __shared__ uint8_t sLut[16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
+  const int n0 = blockIdx.x * TN;
+  const bool zp = g.wz != nullptr;
+  // the GeLU table goes to LDS after the K loop; only its load is issued now
+  uint32_t lutv = 0;
+  if (GELU && tid < 16) lutv = g.lut[tid];
+
+  // Copy j of a stage (A: j < 4 MS, B: j < 4) fills LDS rows 8j .. 8j+7;
+  // lane l writes row 8j + l/8 at position l % 8 and so fetches chunk
+  // (l % 8) ^ swz8(row). Wave w issues A copies w, w + 4, ... and B copy w.
+  // Rows past the matrix edge read its last row (their results are never
+  // stored).
+  const int8_t *ga[MS];
+#pragma unroll
+  for (int i = 0; i < MS; ++i) {
+    const int r = (wave + 4 * i) * 8 + (lane >> 3);
+    ga[i] = g.a + (int64_t)min(r, M - 1) * g.lda + ((lane & 7) ^ swz8(r)) * 16;
+  }
+  const int rb = wave * 8 + (lane >> 3);
+  const int8_t *gb = g.b + (int64_t)min(n0 + rb, N - 1) * g.ldb + ((lane & 7) ^ swz8(rb)) * 16;
+  const uint32_t ldsA = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sA));
+  const uint32_t ldsB = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sB));
+  auto issue = [&](int kt) {
+    const int st = kt % SST;
+    const int k0 = kt * SK;
+#pragma unroll
+    for (int i = 0; i < MS; ++i) dma16(ga[i] + k0, ldsA + st * A_ST + (wave + 4 * i) * 1024);
+    dma16(gb + k0, ldsB + st * B_ST + wave * 1024);
+  };
+
+  // The epilogue's inputs (column parameters, residual, cache position) are
+  // requested first, so their latency is spent under the K loop.
+  // (Rows and columns past the edge read the last ones: no branches, so the
+  // compiler can count these loads instead of waiting for all of them.)
+  const bool active = wave < MS;
+  const int n = n0 + (lane & 31);
+  ColRaw craw;
+  int32_t resv[16];
+  int pos = 0;
+  if (active) {
+    craw = load_col_raw(g, min(n, N - 1));
+    if (EPI == EPI_L32RES) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = min(wave * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), M - 1);
+        resv[r] = g.res[(int64_t)m * g.ldres + min(n, N - 1)];
+      }
+    }
+    if (SCATTER) pos = *sc.pos;
+  }
+
+  // this wave's copies of all but the newest `later` issued stages have landed
+  auto wait_stages = [&](int later) {
+    if (SST >= 6 && later >= 4)
+      wait_vmcnt<4 * DMA_PER_WAVE>();
+    else if (SST >= 5 && later >= 3)
+      wait_vmcnt<3 * DMA_PER_WAVE>();
+    else if (SST >= 4 && later >= 2)
+      wait_vmcnt<2 * DMA_PER_WAVE>();
+    else if (later >= 1)
+      wait_vmcnt<DMA_PER_WAVE>();
+    else
+      wait_vmcnt<0>();
+  };
+  // after this wave's LDS reads have completed, every wave's landed copies
+  // become visible to all (no release fence: it would drain the copies)
+  auto sync = [&]() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // fragment reads: lane l reads row l % 32 of the subtile, logical chunk
+  // 2 ks + l / 32 of the stage
+  const int sw = swz8(lane & 31);
+  // (waves past the m-subtiles recompute subtile 0 and store nothing: the
+  // loop then has no branch, which would move the accumulator out of AGPRs
+  // every iteration)
+  const int aoff = ((active ? wave * 32 : 0) + (lane & 31)) * SK;
+  const int boff = (lane & 31) * SK;
+  auto read_frags = [&](int kt, v4i *fa, v4i *fb) {
+    const int8_t *pa = &sA[(kt % SST) * A_ST + aoff];
+    const int8_t *pb = &sB[(kt % SST) * B_ST + boff];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int p = ((2 * ks + (lane >> 5)) ^ sw) * 16;
+      fa[ks] = *reinterpret_cast<const v4i *>(pa + p);
+      fb[ks] = *reinterpret_cast<const v4i *>(pb + p);
+    }
+  };
+
+  // Software pipeline: while the MFMAs consume stage kt from registers, the
+  // fragments of stage kt + 1 are read from LDS and stages up to kt + SST - 1
+  // are being copied in. Stage kt + SST - 1 overwrites the buffer of stage
+  // kt - 1, whose fragments every wave has consumed before the barrier.
+  const int nk = K / SK;
+#pragma unroll
+  for (int i = 0; i < SST - 1; ++i)
+    if (i < nk) issue(i);
+  wait_stages(min(SST - 2, nk - 1));
+  sync();
+  // two accumulators, so that consecutive MFMAs do not wait on each other
+  v16i acc, acc2;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0;
+  int32_t xs = 0;
+  v4i fa[4], fb[4];
+  read_frags(0, fa, fb);
+  for (int kt = 0; kt < nk; ++kt) {
+    v4i na[4], nb[4];
+    if (kt + 1 < nk) {
+      wait_stages(min(SST - 3, nk - 2 - kt));
+      sync();
+      if (kt + SST - 1 < nk) issue(kt + SST - 1);
+      read_frags(kt + 1, na, nb);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ks += 2) {
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks], fb[ks], acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks + 1], fb[ks + 1], acc2, 0, 0, 0);
+    }
+    if (zp) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) xs = sum16v(fa[ks], xs);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = na[ks];
+      fb[ks] = nb[ks];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = (int32_t)((uint32_t)acc[r] + (uint32_t)acc2[r]);
+  if (zp && active) {
+    xs += __shfl_xor(xs, 32);
+    if (lane < 32) sXs[wave * 32 + lane] = xs;
+  }
+  if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
+  __syncthreads();
+  if (!active) return;
+
+  // Epilogue from registers. 32x32 MFMA layout: lane l holds column l % 32
+  // and, for register r, row (r / 4) * 8 + (l / 32) * 4 + (r % 4).
+  if (n >= N) return;
+  const ColParams c = decode_col<EPI>(g, craw);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = wave * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    if (m < M) {
+      const uint32_t a = corrected_k32k(acc[r], zp ? sXs[m] : 0, c);
+      skinny_store<EPI, GELU, SCATTER>(g, sc, c, sLut, pos, m, n, a, EPI == EPI_L32RES ? resv[r] : 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Register kernel (any K % 16 == 0)
+// ---------------------------------------------------------------------------
+
+constexpr int NT = 512;   // 8 waves
 constexpr int BATCH = 8;  // k32 steps whose loads are in flight together
 constexpr int PLD = 33;   // LDS row stride of the partial sums (words)
 
@@ -63,13 +324,7 @@ __global__ __launch_bounds__(NT) void gemm_skinny_kernel(GemmArgs g, SkinnyScatt
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[u], fb[u], acc, 0, 0, 0);
-      if (zp) {
-        const int ones = 0x01010101;
-        xs = __builtin_amdgcn_sdot4(fa[u][0], ones, xs, false);
-        xs = __builtin_amdgcn_sdot4(fa[u][1], ones, xs, false);
-        xs = __builtin_amdgcn_sdot4(fa[u][2], ones, xs, false);
-        xs = __builtin_amdgcn_sdot4(fa[u][3], ones, xs, false);
-      }
+      if (zp) xs = sum16v(fa[u], xs);
     }
   }
 
@@ -101,41 +356,18 @@ __global__ __launch_bounds__(NT) void gemm_skinny_kernel(GemmArgs g, SkinnyScatt
       a += (uint32_t)sPart[((s * ms + mi) * 32 + mr) * PLD + cl];
       if (zp) xsum += sXs[s * ms + mi][mr];
     }
-    a = corrected((int32_t)a, xsum, c);
-    if (EPI == EPI_L8 || EPI == EPI_S8) {
-      int32_t y = clampi(apply_shift(mulh_su((int32_t)a, c.mult), c.shift), -127, 127);
-      if (GELU) y = gelu_dec(y, sLut, c);
-      if (SCATTER) {
-        // columns [0, C): Q; [C, 2C): K appended at position pos + (m % T)
-        // of the [B, H, T_cache, D] cache; [2C, 3C): V appended to the
-        // transposed [B, H, D, T_cache] cache
-        const int b = m / sc.T, t = pos + m % sc.T;
-        if (n < sc.C) {
-          sc.q[(int64_t)m * sc.ldq + n] = (int8_t)y;
-        } else if (t < 0 || t >= sc.t_cap) {
-          // position outside the cache: nothing is appended
-        } else if (n < 2 * sc.C) {
-          const int h = (n - sc.C) / sc.D, d = (n - sc.C) % sc.D;
-          sc.k[(int64_t)b * sc.k_sb + (int64_t)h * sc.k_sh + (int64_t)t * sc.k_st + d] = (int8_t)y;
-        } else {
-          const int h = (n - 2 * sc.C) / sc.D, d = (n - 2 * sc.C) % sc.D;
-          sc.v[(int64_t)b * sc.v_sb + (int64_t)h * sc.v_sh + (int64_t)d * sc.v_sd + t] = (int8_t)y;
-        }
-      } else {
-        reinterpret_cast<int8_t *>(g.out)[(int64_t)m * g.ldc + n] = (int8_t)y;
-      }
-    } else {
-      const int32_t br = (int32_t)((uint32_t)mulh_su((int32_t)a, c.mult) << c.shift.sh);
-      if (EPI == EPI_L32) {
-        reinterpret_cast<int32_t *>(g.out)[(int64_t)m * g.ldc + n] = br;
-      } else {
-        const int32_t res = g.res[(int64_t)m * g.ldres + n];
-        const uint32_t v = (uint32_t)br + (uint32_t)(res * (int32_t)g.res_mult);
-        const int32_t y = clampi(rshift_pos((int32_t)v, 15), -16383, 16383);
-        reinterpret_cast<int16_t *>(g.out)[(int64_t)m * g.ldc + n] = (int16_t)y;
-      }
-    }
+    const int32_t res = EPI == EPI_L32RES ? g.res[(int64_t)m * g.ldres + n] : 0;
+    skinny_store<EPI, GELU, SCATTER>(g, sc, c, sLut, pos, m, n, corrected((int32_t)a, xsum, c), res);
   }
+}
+
+constexpr int64_t kDeepRingTiles = 256;  // CUs of an MI355X
+
+bool lds_eligible(const GemmArgs &g) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b) |
+                       (uintptr_t)g.lda | (uintptr_t)g.ldb;
+  // corrected_k32k needs K <= 32768
+  return g.K % SK == 0 && g.K <= 32768 && (al & 15) == 0;
 }
 
 template <int EPI, bool GELU, bool SCATTER>
@@ -143,6 +375,26 @@ int launch_skinny(const GemmArgs &g, const SkinnyScatter &sc, hipStream_t s) {
   const int64_t tiles = (g.N + TN - 1) / TN;
   if (tiles == 0 || g.M == 0) return 0;
   const int ms = (int)((g.M + 31) / 32);
+  if (lds_eligible(g)) {
+    const dim3 grid((unsigned)tiles), block(LNT);
+    // one block per CU: 6 stages (up to 120 KB of LDS); more blocks: 3
+    const bool deep = tiles <= kDeepRingTiles;
+#define IW_SKL(MS_)                                                                                 \
+  do {                                                                                              \
+    if (deep)                                                                                       \
+      hipLaunchKernelGGL((gemm_skinny_lds_kernel<EPI, GELU, SCATTER, MS_, 6>), grid, block, 0, s, g, sc); \
+    else                                                                                            \
+      hipLaunchKernelGGL((gemm_skinny_lds_kernel<EPI, GELU, SCATTER, MS_, 3>), grid, block, 0, s, g, sc); \
+  } while (0)
+    if (ms <= 1)
+      IW_SKL(1);
+    else if (ms <= 2)
+      IW_SKL(2);
+    else
+      IW_SKL(4);
+#undef IW_SKL
+    return check_launch("gemm_skinny_lds_kernel");
+  }
   const int msp = ms <= 1 ? 1 : (ms <= 2 ? 2 : 4);  // m-subtiles per block: a divisor of 8
   hipLaunchKernelGGL((gemm_skinny_kernel<EPI, GELU, SCATTER>), dim3((unsigned)tiles), dim3(NT), 0, s,
                      g, sc, msp);

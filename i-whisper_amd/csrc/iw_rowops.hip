@@ -43,10 +43,36 @@ __global__ __launch_bounds__(256) void layernorm32_kernel(
     int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int64_t rows, int hidden,
     int code) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nch = hidden >> 2;
   const int16_t *xr = x + row * hidden;
+  // gamma / beta of this lane's columns are requested with the row, so their
+  // latency hides behind the reductions
+  const bool g_al = (reinterpret_cast<uintptr_t>(gamma) & 3) == 0;
+  const bool b_al = beta && (reinterpret_cast<uintptr_t>(beta) & 15) == 0;
+  uint32_t gw[LN_MAX_CHUNKS];
+  uint4 bw[LN_MAX_CHUNKS];
+#pragma unroll
+  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+    const int ch = lane + 64 * c;
+    gw[c] = 0;
+    bw[c] = make_uint4(0, 0, 0, 0);
+    if (ch < nch) {
+      if (g_al) {
+        gw[c] = *reinterpret_cast<const uint32_t *>(gamma + ch * 4);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gw[c] |= (uint32_t)(uint8_t)gamma[ch * 4 + e] << (8 * e);
+      }
+      if (b_al) {
+        bw[c] = *reinterpret_cast<const uint4 *>(beta + ch * 4);
+      } else if (beta) {
+        bw[c] = make_uint4((uint32_t)beta[ch * 4], (uint32_t)beta[ch * 4 + 1],
+                           (uint32_t)beta[ch * 4 + 2], (uint32_t)beta[ch * 4 + 3]);
+      }
+    }
+  }
   int32_t v[LN_MAX_CHUNKS][4];
   uint32_t sum = 0;
 #pragma unroll
@@ -99,14 +125,13 @@ __global__ __launch_bounds__(256) void layernorm32_kernel(
     const int ch = lane + 64 * c;
     if (ch < nch) {
       uint32_t packed = 0;
+      const uint32_t bv[4] = {bw[c].x, bw[c].y, bw[c].z, bw[c].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int col = ch * 4 + e;
         const int32_t d = v[c][e] - mean;
         uint32_t t = (uint32_t)d * (uint32_t)inv * ln_m;
         int32_t y = clampi(rshift((int32_t)t, nshift), -16383, 16383);
-        uint32_t a = (uint32_t)y * (uint32_t)(int32_t)gamma[col];
-        if (beta) a += (uint32_t)beta[col];
+        uint32_t a = (uint32_t)y * (uint32_t)(int32_t)(int8_t)(gw[c] >> (8 * e)) + bv[e];
         int32_t o = clampi(rshift(mulh((int32_t)a, out_m), (uint32_t)out_s), -127, 127);
         packed |= ((uint32_t)(uint8_t)(int8_t)o) << (8 * e);
       }
@@ -324,8 +349,11 @@ int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *bet
   const int code = layernorm_width_code(hidden);
   if (code < 0) return fail("unsupported LayerNorm hidden size: " + std::to_string(hidden));
   if (rows == 0) return 0;
-  const int64_t blocks = (rows + 3) / 4;
-  hipLaunchKernelGGL(layernorm32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, gamma, beta,
+  // one row per wave; few rows (a decode step) get a block each, so they
+  // spread over as many CUs as there are rows
+  const int per_block = rows >= 4096 ? 4 : 1;
+  const int64_t blocks = (rows + per_block - 1) / per_block;
+  hipLaunchKernelGGL(layernorm32_kernel, dim3((unsigned)blocks), dim3(64 * per_block), 0, s, x, gamma, beta,
                      (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, rows,
                      (int)hidden, code);
   return check_launch("layernorm32_kernel");

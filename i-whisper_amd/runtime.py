@@ -215,6 +215,7 @@ class DecoderRunner:
         self.hist_cols = max_steps or decoder.n_ctx
         self.history = torch.zeros((batch, self.hist_cols), dtype=torch.int64, device=dev)
         self.graph = None
+        self.graph_stream = None
 
     # ---- per utterance ----
     def set_audio(self, xa: torch.Tensor):
@@ -345,14 +346,18 @@ class DecoderRunner:
                 self.decode_step()
             return
         if self.graph is None:
-            # one eager step loads every kernel before capture
-            self.decode_step()
-            n -= 1
-            torch.cuda.current_stream().synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
+            # one eager step on the capture stream loads every kernel and
+            # creates that stream's split-K GEMM workspace before capture
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
                 self.decode_step()
-            self.graph = g
+            n -= 1
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                self.decode_step()
+            self.graph, self.graph_stream = g, s
         for _ in range(n):
             self.graph.replay()
 

@@ -34,6 +34,8 @@ GEMM_SHAPES = [
     (1, 1, 1), (3, 15, 5), (7, 16, 9), (5, 17, 33), (33, 31, 64), (64, 32, 128),
     (65, 33, 129), (128, 64, 128), (129, 100, 130), (200, 128, 96), (256, 1280, 384),
     (300, 512, 1536), (1, 1280, 1280), (128, 1280, 1280),
+    # decode shapes split over K across blocks (ragged M, few column tiles)
+    (100, 2048, 200), (32, 4096, 64), (128, 5120, 1280), (64, 1280, 3840),
 ]
 
 
@@ -84,7 +86,8 @@ def test_linear8_gelu(iw, oracle, gpu, M, K, N, pc):
     assert np.array_equal(host(got), exp)
 
 
-@pytest.mark.parametrize("M,K,N", [(5, 17, 33), (128, 64, 128), (300, 2048, 512), (129, 5120, 1280)])
+@pytest.mark.parametrize("M,K,N", [(5, 17, 33), (128, 64, 128), (300, 2048, 512), (129, 5120, 1280),
+                                   (128, 5120, 1280), (77, 1280, 1280)])
 def test_linear32_residual15(iw, oracle, gpu, M, K, N):
     _print_case("linear32_residual15", M, K, N)
     x, w, b, z, m, s = gen.realistic_linear_case(M * 3 + K + N, M, K, N)
@@ -188,6 +191,25 @@ def test_layernorm32(iw, oracle, gpu, hidden, rows, spread):
         torch.tensor([om], dtype=torch.uint32), torch.tensor([os_], dtype=torch.int8))
     exp = oracle.layernorm32(x, g, b, lm, ls, om, os_)
     assert np.array_equal(host(got), exp)
+
+
+@pytest.mark.parametrize("rows", [3, 5000])
+def test_layernorm32_unaligned_params(iw, oracle, gpu, rows):
+    """gamma / beta views at odd offsets, and no beta at all."""
+    hidden = 1280
+    _print_case("layernorm32 unaligned", rows)
+    x, g, b, lm, ls, om, os_ = gen.ln_case(rows + 7, rows, hidden, 3000)
+    gbuf = torch.zeros(hidden + 1, dtype=torch.int8, device="cuda")
+    gbuf[1:] = T(g)
+    bbuf = torch.zeros(hidden + 1, dtype=torch.int32, device="cuda")
+    bbuf[1:] = T(b)
+    scal = (torch.tensor([lm], dtype=torch.uint8), torch.tensor([ls], dtype=torch.int8),
+            torch.tensor([om], dtype=torch.uint32), torch.tensor([os_], dtype=torch.int8))
+    xt = T(x)
+    got = iw.kernels.layernorm32_hip(xt, gbuf[1:], bbuf[1:], *scal)
+    assert np.array_equal(host(got), oracle.layernorm32(x, g, b, lm, ls, om, os_))
+    got = iw.kernels.layernorm32_hip(xt, gbuf[1:], None, *scal)
+    assert np.array_equal(host(got), oracle.layernorm32(x, g, None, lm, ls, om, os_))
 
 
 def test_layernorm32_rejects_width(iw, gpu):
