@@ -277,6 +277,154 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_lds_kernel(GemmArgs g, Skinny
 }
 
 // ---------------------------------------------------------------------------
+// M-split kernel: one 32-row m-subtile x 32 columns per block
+// ---------------------------------------------------------------------------
+//
+// For decode grids (tiles x m-subtiles up to a few CUs' worth) each block
+// takes one 32 x 32 output tile over all of K, so it copies 32 x K bytes of
+// A and 32 x K of B instead of M x K of A. Stage s (128 K bytes: 4 KB of A,
+// 4 KB of B) belongs to wave s % 4, which copies it into its own LDS ring,
+// reads its fragments back and runs its four MFMAs: the four waves are
+// independent pipelines with no barrier in the K loop. Their partial tiles
+// are added in LDS (the rings' space) at the end. The blocks of one column
+// tile share blockIdx % 8, i.e. one XCD, so its B rows come from HBM once.
+template <int EPI, bool GELU, bool SCATTER, int WST>
+__global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, SkinnyScatter sc, int ms,
+                                                                 int tiles) {
+  constexpr int STB = 8192;  // bytes per stage: A rows then B rows, 128 bytes each
+  constexpr int PLDM = 33;
+  __shared__ __attribute__((aligned(1024))) int8_t sRing[4 * WST * STB];
+  __shared__ int32_t sXs[4][32];
+  __shared__ uint8_t sLut[16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bid = blockIdx.x;
+  const int tile = (bid & 7) + 8 * (bid / (8 * ms));
+  const int msub = (bid >> 3) % ms;
+  if (tile >= tiles) return;
+  const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
+  const int n0 = tile * TN, m0 = msub * 32;
+  const bool zp = g.wz != nullptr;
+
+  // epilogue inputs, requested before the K loop: thread t serves column
+  // t % 32 and rows t / 32 + 8 j of the subtile
+  const int cl = tid & 31;
+  const int n = n0 + cl;
+  const int mr0 = tid >> 5;
+  uint32_t lutv = 0;
+  if (GELU && tid < 16) lutv = g.lut[tid];
+  const ColRaw craw = load_col_raw(g, min(n, N - 1));
+  int32_t resv[4];
+  if (EPI == EPI_L32RES) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      resv[j] = g.res[(int64_t)min(m0 + mr0 + 8 * j, M - 1) * g.ldres + min(n, N - 1)];
+  }
+  int pos = 0;
+  if (SCATTER) pos = *sc.pos;
+
+  // copy j of a stage (j < 4: A, else B) fills rows 8 (j % 4) .. +7 of its
+  // half; lane l writes row 8 (j % 4) + l / 8 at position l % 8, fetching
+  // chunk (l % 8) ^ swz8(row)
+  const int r8 = lane >> 3;
+  const int8_t *ga[4];
+  const int8_t *gb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 8 * j + r8;
+    const int c = ((lane & 7) ^ swz8(r)) * 16;
+    ga[j] = g.a + (int64_t)min(m0 + r, M - 1) * g.lda + c;
+    gb[j] = g.b + (int64_t)min(n0 + r, N - 1) * g.ldb + c;
+  }
+  const uint32_t ring =
+      __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sRing)) + wave * WST * STB;
+  const int nk = K / SK;
+  const int mine = nk > wave ? (nk - wave + 3) / 4 : 0;  // stages wave, wave + 4, ...
+  auto issue = [&](int t) {
+    const int64_t k0 = (int64_t)(wave + 4 * t) * SK;
+    const uint32_t dst = ring + (t % WST) * STB;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(ga[j] + k0, dst + j * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(gb[j] + k0, dst + 4096 + j * 1024);
+  };
+#pragma unroll
+  for (int t = 0; t < WST - 1; ++t)
+    if (t < mine) issue(t);
+
+  const int sw = swz8(lane & 31);
+  const int8_t *wr = sRing + wave * WST * STB + (lane & 31) * SK;
+  v16i acc, acc2;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0;
+  int32_t xs = 0;
+  for (int t = 0; t < mine; ++t) {
+    // stage t has landed once the copies of at most min(WST - 2, mine - 1 - t)
+    // later stages are outstanding
+    const int later = min(WST - 2, mine - 1 - t);
+    if (WST >= 4 && later >= 2)
+      wait_vmcnt<16>();
+    else if (later >= 1)
+      wait_vmcnt<8>();
+    else
+      wait_vmcnt<0>();
+    const int8_t *pa = wr + (t % WST) * STB;
+    v4i fa[4], fb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int p = ((2 * ks + (lane >> 5)) ^ sw) * 16;
+      fa[ks] = *reinterpret_cast<const v4i *>(pa + p);
+      fb[ks] = *reinterpret_cast<const v4i *>(pa + 4096 + p);
+    }
+    // the slot of stage t - 1 is free: its fragments were consumed
+    if (t + WST - 1 < mine) issue(t + WST - 1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ks += 2) {
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks], fb[ks], acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks + 1], fb[ks + 1], acc2, 0, 0, 0);
+    }
+    if (zp) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) xs = sum16v(fa[ks], xs);
+    }
+  }
+  if (zp) {
+    xs += __shfl_xor(xs, 32);
+    if (lane < 32) sXs[wave][lane] = xs;
+  }
+  // partial tiles into the (now idle) rings: [wave][row][PLDM]
+  __syncthreads();
+  int32_t *part = reinterpret_cast<int32_t *>(sRing) + wave * 32 * PLDM;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    part[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PLDM + (lane & 31)] =
+        (int32_t)((uint32_t)acc[r] + (uint32_t)acc2[r]);
+  if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
+  __syncthreads();
+
+  if (n >= N) return;
+  const ColParams c = decode_col<EPI>(g, craw);
+  const int32_t *ps = reinterpret_cast<const int32_t *>(sRing);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = mr0 + 8 * j;
+    const int m = m0 + r;
+    if (m < M) {
+      uint32_t a = 0;
+      int32_t xsum = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        a += (uint32_t)ps[(w * 32 + r) * PLDM + cl];
+        if (zp) xsum += sXs[w][r];
+      }
+      skinny_store<EPI, GELU, SCATTER>(g, sc, c, sLut, pos, m, n, corrected_k32k((int32_t)a, xsum, c),
+                                       EPI == EPI_L32RES ? resv[j] : 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Register kernel (any K % 16 == 0)
 // ---------------------------------------------------------------------------
 
@@ -362,6 +510,8 @@ __global__ __launch_bounds__(NT) void gemm_skinny_kernel(GemmArgs g, SkinnyScatt
 }
 
 constexpr int64_t kDeepRingTiles = 256;  // CUs of an MI355X
+// grids up to this many 32 x 32 tiles take the m-split kernel
+constexpr int64_t kMsplitMaxBlocks = 1024;
 
 bool lds_eligible(const GemmArgs &g) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.b) |
@@ -375,6 +525,17 @@ int launch_skinny(const GemmArgs &g, const SkinnyScatter &sc, hipStream_t s) {
   const int64_t tiles = (g.N + TN - 1) / TN;
   if (tiles == 0 || g.M == 0) return 0;
   const int ms = (int)((g.M + 31) / 32);
+  if (lds_eligible(g) && tiles * ms <= kMsplitMaxBlocks) {
+    // one 32 x 32 tile per block; blocks of a column tile share an XCD
+    const dim3 grid((unsigned)(((tiles + 7) / 8) * 8 * ms)), block(LNT);
+    if (tiles * ms <= kDeepRingTiles)
+      hipLaunchKernelGGL((gemm_skinny_msplit_kernel<EPI, GELU, SCATTER, 4>), grid, block, 0, s, g, sc, ms,
+                         (int)tiles);
+    else
+      hipLaunchKernelGGL((gemm_skinny_msplit_kernel<EPI, GELU, SCATTER, 2>), grid, block, 0, s, g, sc, ms,
+                         (int)tiles);
+    return check_launch("gemm_skinny_msplit_kernel");
+  }
   if (lds_eligible(g)) {
     const dim3 grid((unsigned)tiles), block(LNT);
     // one block per CU: 6 stages (up to 120 KB of LDS); more blocks: 3
