@@ -7,9 +7,19 @@ an integer checkpoint. One step = encoder over the batch + the whole greedy
 decode; inputs are resident in HBM before the timed region.
 
 Prints one JSON line: end-to-end audio-seconds/s as ``value``, plus encoder
-audio-s/s, decoder tokens/s, the encoder-GEMM int8 MFMA roofline fraction
-(HIP events around every encoder GEMM launch in the timed steps) and the CPU
-oracle timed on a bounded sample on the host.
+audio-s/s, decoder tokens/s, two roofline objects and the CPU oracle timed on a
+bounded sample on the host:
+
+* ``roofline``: the kernel with the largest share of the step, the decoder's
+  cross-attention over the cached audio K/V (HBM-bound). Its launches inside
+  the timed steps run in a replayed HIP graph, so its duration is taken right
+  after the timed region from launches identical to the graph's (same kernel,
+  same buffers, same stream) bracketed by HIP events on that stream.
+  ``traffic`` is the HBM bytes per launch from rocprofv3 FETCH_SIZE and
+  WRITE_SIZE counters, scaled by the same counters on a plain copy, as
+  recorded in profiles/attn_decode_cross_b128_pmc.md.
+* ``roofline_encoder_gemm``: the encoder GEMMs (int8 MFMA), HIP events around
+  every encoder GEMM launch in the timed steps.
 """
 from __future__ import annotations
 
@@ -43,8 +53,8 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: int = 4,
-                 dec_steps: int = 12) -> dict:
+def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: int = 8,
+                 dec_steps: int = 96) -> dict:
     """The oracle on the host for one sample: the encoder front end, ``enc_blocks``
     of the encoder blocks and ``dec_steps`` greedy steps, scaled to the full
     per-sample workload (all blocks, all steps)."""
@@ -74,10 +84,44 @@ def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: i
         "value": round(30.0 / (enc + dec), 5), "unit": "audio-s/s", "cores": threads, "kind": "port",
         "sample": (f"oracle (oracle/iw_oracle.c, OpenMP GEMM/attention loops) on one 30 s sample: "
                    f"encoder front end + {nb}/{dims.n_audio_layer} blocks scaled to all blocks, "
-                   f"{nd}/{steps_total} greedy steps scaled to all steps; "
+                   f"the first {nd}/{steps_total} greedy steps scaled to all steps; "
                    f"measured {t3 - t0 + (dec * nd / max(steps_total, 1)):.1f} s"),
         "encoder_s_per_sample": round(enc, 3), "decoder_s_per_sample": round(dec, 3),
     }
+
+
+PMC_SUMMARY = ROOT / "profiles" / "attn_decode_cross_b128_pmc.md"
+
+
+def recorded_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (a line ``traffic_bytes_per_launch <kernel>: <bytes>``), or None."""
+    try:
+        for line in PMC_SUMMARY.read_text().splitlines():
+            if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
+def cross_attention_probe(dec, dims, batch: int, launches: int = 20) -> float:
+    """Average duration (ms) of the decoder cross-attention kernel on layer 0's
+    cached K/V, HIP events on the launch stream around each launch."""
+    import torch
+
+    C = dims.n_text_state
+    q = torch.randint(-127, 128, (batch, C), dtype=torch.int8, device="cuda")
+    out = torch.empty((batch, C), dtype=torch.int8, device="cuda")
+    dec.cross_attention(0, q, out)  # warm
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(launches)]
+    for e0, e1 in ev:
+        e0.record()
+        dec.cross_attention(0, q, out)
+        e1.record()
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / launches
 
 
 def main():
@@ -148,6 +192,8 @@ def main():
             log(f"[bench] timed step {k + 1}/{args.steps} queued")
         torch.cuda.synchronize()
         wall = time.perf_counter() - t_start
+        if dsteps:
+            xa_ms = cross_attention_probe(dec, dims, batch)
     enc_ms = sum(e0.elapsed_time(e1) for e0, e1, _, _ in evs)
     dec_ms = sum(e1.elapsed_time(e2) for _, e1, e2, _ in evs)
     K = args.steps
@@ -181,11 +227,25 @@ def main():
         "encoder_ms_per_step": round(enc_ms / K, 3),
         "decoder_ms_per_step": round(dec_ms / K, 3),
         "encoder_attention_tops": round(a_tops, 1),
-        "roofline": {"bound": "mfma", "kernel": "gemm_i8_kernel (encoder QKV/out/FC1/FC2 launches)",
-                     "achieved": round(g_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-                     "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                     "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4)},
+        "roofline_encoder_gemm": {
+            "bound": "mfma", "kernel": "gemm_dtl_kernel (encoder QKV/out/FC1/FC2 launches)",
+            "achieved": round(g_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+            "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+            "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4)},
     }
+    if dsteps:
+        # algorithmic bytes: K [Tk, D] and V [D, Tk] of every (b, h), q and out
+        H, D, Tk = dims.n_text_head, dims.n_text_state // dims.n_text_head, dims.n_audio_ctx
+        xa_bytes = batch * H * (2 * Tk * D + 2 * D)
+        xa_gbs = xa_bytes / (xa_ms * 1e-3) / 1e9
+        kname = "attn_decode_stream_kernel<2048, 8>"
+        result["roofline"] = {
+            "bound": "hbm", "kernel": kname + " (decoder cross-attention, 1 query x "
+                     f"{Tk} cached keys per (batch, head))",
+            "achieved": round(xa_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(xa_gbs / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(kname),
+            "bytes_per_launch": xa_bytes, "avg_launch_ms": round(xa_ms, 4),
+            "launches_per_step": dsteps * dims.n_text_layer}
     del model, enc, dec
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:

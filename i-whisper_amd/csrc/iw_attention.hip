@@ -867,7 +867,11 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
                        (uintptr_t)a.k_sb | (uintptr_t)a.v_sd | (uintptr_t)a.v_sh | (uintptr_t)a.v_sb |
                        (uintptr_t)a.q_sb;
   if (a.D == 64 && (al & 15) == 0 && a.max_tk <= DC_MAX_TK) {
-    if (a.max_tk <= 2048)
+    // (self-attention caches up to 512 positions get their own, smaller
+    // instance, so profiles separate it from cross-attention)
+    if (a.max_tk <= 512)
+      hipLaunchKernelGGL((attn_decode_stream_kernel<512, 8>), grid, dim3(256), 0, s, a, pos);
+    else if (a.max_tk <= 2048)
       hipLaunchKernelGGL((attn_decode_stream_kernel<2048, 8>), grid, dim3(256), 0, s, a, pos);
     else
       hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, 8>), grid, dim3(256), 0, s, a, pos);

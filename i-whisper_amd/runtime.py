@@ -251,6 +251,12 @@ class DecoderRunner:
                       s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset,
                       table.data_ptr(), False, _stream())
 
+    def cross_attention(self, layer: int, q: torch.Tensor, out: torch.Tensor):
+        """One decode-step cross-attention of ``layer`` over this utterance's
+        cached K/V: q and out are [B, C] int8 (launched on the current stream)."""
+        att = self.dec.blocks[layer].cross_attn
+        self._cross_attend(att, layer, q.data_ptr(), self.C, self.C, 1, out, None)
+
     def _finish(self, x_last: torch.Tensor, pos_inc: int):
         """Final LayerNorm of the last position, classifier, argmax, record, advance."""
         dec = self.dec
@@ -346,8 +352,8 @@ class DecoderRunner:
                 self.decode_step()
             return
         if self.graph is None:
-            # one eager step on the capture stream loads every kernel and
-            # creates that stream's split-K GEMM workspace before capture
+            # one eager step on the capture stream loads every kernel before
+            # capture
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(s):

@@ -237,6 +237,66 @@ int iw_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
 int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                    iw_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Decode step over preallocated KV caches with the cache position on the
+ * device (*pos), so that one captured step replays for every token.
+ * Replaces the reference's per-step chain: TextDecoder_int.forward with
+ * offset = cached length (model_int.py:1398-1442), the hook-side torch.cat
+ * of the self-attention K/V (model_int.py:1587-1618), the cross-attention
+ * K/V reuse (model_int.py:722-730) and GreedyDecoder.update
+ * (decoding.py:280-296). Cache layouts: K [b][h][t][d] at
+ * k + b*k_sb + h*k_sh + t*k_st + d; V transposed per head [b][h][d][t] at
+ * v + b*v_sb + h*v_sh + d*v_sd + t.
+ * ------------------------------------------------------------------------- */
+
+/* Self-attention Q/K/V projection (MultiHeadAttention_int.forward,
+ * model_int.py:720-726) as one Linear8 over the concatenated [3C, K] weight:
+ * columns [0, C) go to q_out[m*q_ld + c]; columns [C, 2C) (K) and [2C, 3C)
+ * (V) of row m = b*T + i are appended at cache position t = *pos + i
+ * (T = tokens_per_row_group), dropped when t >= cache_positions. */
+int iw_linear8_qkv_cache(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                         const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                         int64_t M, int64_t K, bool has_bias, bool asymmetric, int8_t *q_out,
+                         int64_t q_ld, int8_t *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                         int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
+                         int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
+                         const int32_t *pos, iw_stream_t stream);
+
+/* One-query attention over the caches (qkv_attention for q_length 1,
+ * model_int.py:774-1040): q [b][h*D] at q + b*q_sb, out at out + b*o_sb.
+ * The key count is min(k_length + *pos, max_keys) (pos may be NULL when
+ * max_keys == k_length); max_keys <= 4096, v_sd covers round_up(max_keys, 16). */
+int iw_attention_decode_cache(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
+                              int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
+                              int64_t v_sh, int64_t v_sd, int8_t *out, int64_t o_sb, int64_t batch,
+                              int64_t heads, int64_t head_dim, int64_t k_length,
+                              const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
+                              int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
+                              int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream);
+
+/* Decoder input of one token per row at position *pos (model_int.py:1408-1425):
+ * out[b, c] = add_requant15(table[tokens[b], c], pe[min(*pos, pe_rows - 1), c]). */
+int iw_embed_tokens(const int64_t *tokens, const int8_t *table, const int8_t *pe,
+                    int64_t pe_rows, const int32_t *pos, const uint16_t *multiplier,
+                    const int8_t *shift, int16_t *out, int64_t batch, int64_t channels,
+                    iw_stream_t stream);
+
+/* Greedy step bookkeeping (GreedyDecoder.update, decoding.py:280-296, on the
+ * int8 logits): next_tokens[r] = first argmax of row r; when *step <
+ * history_cols, history[r*history_ld + *step] = next_tokens[r]; then
+ * *step += 1 and *pos += pos_increment. */
+int iw_greedy_advance(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld,
+                      int64_t *next_tokens, int64_t *history, int64_t history_ld,
+                      int64_t history_cols, int32_t *step, int32_t *pos, int32_t pos_increment,
+                      iw_stream_t stream);
+
+/* Per-head gather into a [b][h][t][d] cache (the cross-attention K of
+ * model_int.py:722-730, computed once per utterance):
+ * dst[b*dst_sb + h*dst_sh + (t_offset+t)*dst_st + d] = src[b*src_sb + t*src_st + h*D + d]. */
+int iw_gather_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst, int64_t dst_sb,
+                    int64_t dst_sh, int64_t dst_st, int64_t t_offset, int64_t batch,
+                    int64_t positions, int64_t heads, int64_t head_dim, iw_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
