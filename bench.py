@@ -11,7 +11,7 @@ audio-s/s, decoder tokens/s, two roofline objects and the CPU oracle timed on a
 bounded sample on the host:
 
 * ``roofline``: the kernel with the largest share of the step, the decoder's
-  cross-attention over the cached audio K/V (HBM-bound). Its launches inside
+  cross-attention over the cached audio K/V (HBM-bound, ``XA_KERNEL``). Its launches inside
   the timed steps run in a replayed HIP graph, so its duration is taken right
   after the timed region from launches identical to the graph's (same kernel,
   same buffers, same stream) bracketed by HIP events on that stream.
@@ -91,6 +91,9 @@ def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: i
 
 
 PMC_SUMMARY = ROOT / "profiles" / "attn_decode_cross_b128_pmc.md"
+# the decoder cross-attention kernel as profilers name it (key capacity, ring
+# slots, keys per chunk)
+XA_KERNEL = "attn_decode_stream_kernel<2048, 3, 128>"
 
 
 def recorded_traffic(kernel: str):
@@ -238,7 +241,7 @@ def main():
         H, D, Tk = dims.n_text_head, dims.n_text_state // dims.n_text_head, dims.n_audio_ctx
         xa_bytes = batch * H * (2 * Tk * D + 2 * D)
         xa_gbs = xa_bytes / (xa_ms * 1e-3) / 1e9
-        kname = "attn_decode_stream_kernel<2048, 8>"
+        kname = XA_KERNEL
         result["roofline"] = {
             "bound": "hbm", "kernel": kname + " (decoder cross-attention, 1 query x "
                      f"{Tk} cached keys per (batch, head))",

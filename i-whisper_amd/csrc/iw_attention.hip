@@ -619,14 +619,14 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 // One block per (batch, head) reads Tk x 64 bytes of K and 64 x Tk bytes of
 // V^T, nothing else of size, so the kernel is HBM-bound and a CU needs many
 // bytes in flight (bandwidth x latency). Both operands flow through one ring
-// of NR 4 KB slots in 64-key chunks: K chunks 0 .. nK-1, then V^T chunks, so
-// the copies of V are already under way while the row maximum and P are
-// formed. Each chunk is one global_load_lds_dwordx4 per wave, and every lane
-// later reads back exactly the 16 bytes it copied (K: key w*16 + l/4, bytes
-// 16 (l%4); V^T: row d = w*16 + l/4, keys 16 (l%4) of the chunk), so a wave
-// only waits for its own copies (vmcnt) and the ring needs no barrier.
-// Keys past Tk read the last valid key / chunk; their scores are dropped and
-// their P is 0.
+// of NR slots in CH-key chunks: K chunks 0 .. nK-1, then V^T chunks, so the
+// copies of V are already under way while the row maximum and P are formed.
+// A chunk is DPC = CH / 64 global_load_lds_dwordx4 copies per wave, and every
+// lane later reads back exactly the 16-byte pieces it copied (K: one key's
+// 16 (l % 4)-th piece; V^T: one d-row's piece of 16 keys), so a wave only
+// waits for its own copies (vmcnt) and the ring needs no barrier. Keys past
+// Tk read the last valid key / piece; their scores are dropped and their P
+// is 0.
 // ---------------------------------------------------------------------------
 
 template <int N>
@@ -634,13 +634,13 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// s_waitcnt vmcnt(n) for a run-time n in [0, N]
-template <int N>
+// s_waitcnt vmcnt(n * F) for a run-time n in [0, N]
+template <int N, int F>
 __device__ __forceinline__ void wait_vm_upto(int n) {
   if (n >= N) {
-    wait_vm<N>();
+    wait_vm<N * F>();
   } else if constexpr (N > 0) {
-    wait_vm_upto<N - 1>(n);
+    wait_vm_upto<N - 1, F>(n);
   }
 }
 
@@ -662,10 +662,25 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int MAXK, int NR>
+// 128-key chunks in a 3-slot ring (24 KB): measured fastest among chunks of
+// 64 / 128 / 256 keys and rings of 2 to 10 slots (several small blocks per CU
+// hide each block's row-maximum pause better than one deep ring).
+#ifndef IW_DS_NR
+#define IW_DS_NR 3
+#endif
+#ifndef IW_DS_CH
+#define IW_DS_CH 128
+#endif
+
+template <int MAXK, int NR, int CH>
 __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
-  constexpr int D = 64, CH = 64;
-  __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * 4096];
+  constexpr int D = 64;
+  constexpr int DPC = CH / 64;        // copies per wave per chunk
+  constexpr int SLOT = 4096 * DPC;    // bytes per ring slot
+  constexpr int WB = 1024 * DPC;      // bytes per wave per slot
+  constexpr int LPR = 4 * DPC;        // lanes per V^T row piece set
+  constexpr int RPD = 64 / LPR;       // V^T rows per copy
+  __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
   __shared__ int16_t sS[MAXK];  // requantized scores
   __shared__ __attribute__((aligned(16))) uint8_t sP[MAXK];
   __shared__ int32_t sRed[4];
@@ -682,34 +697,47 @@ __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, con
   const int T = 2 * nK;
   if (tid == 0) sHi = 0;
 
-  const int kl = wave * 16 + (lane >> 2);  // key (K) or d-row (V^T) within a chunk
-  const int cq = lane & 3;                 // 16-byte piece
+  // K: copy u of a chunk brings keys wave*16*DPC + 16 u + l/4, piece l % 4
+  const int cq = lane & 3;
+  const int kkey = wave * 16 * DPC + (lane >> 2);
   const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh + cq * 16;
-  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)kl * a.v_sd;
+  // V^T: copy u brings row wave*16 + u*RPD + l/LPR, keys 16 (l % LPR) .. +16
+  const int vp = lane % LPR;
+  const int vrow = wave * 16 + lane / LPR;
+  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)vrow * a.v_sd;
   const int vlast = Tk > 0 ? ((Tk - 1) & ~15) : 0;  // last V^T piece holding a valid key
   const uint32_t ring =
-      __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sRing)) + wave * 1024;
+      __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sRing)) + wave * WB;
   auto issue = [&](int i) {
-    const uint32_t dst = ring + (i % NR) * 4096;
+    const uint32_t dst = ring + (i % NR) * SLOT;
     if (i < nK) {
-      const int j = min(i * CH + kl, Tk - 1);
-      dma16_lds(kb + (int64_t)j * a.k_st, dst);
+#pragma unroll
+      for (int u = 0; u < DPC; ++u)
+        dma16_lds(kb + (int64_t)min(i * CH + kkey + 16 * u, Tk - 1) * a.k_st, dst + u * 1024);
     } else {
-      dma16_lds(vb + min((i - nK) * CH + cq * 16, vlast), dst);
+#pragma unroll
+      for (int u = 0; u < DPC; ++u)
+        dma16_lds(vb + (int64_t)u * RPD * a.v_sd + min((i - nK) * CH + vp * 16, vlast), dst + u * 1024);
     }
   };
 
   // q: lane l needs bytes 16 (l % 4) of the head's 64. It is copied first,
   // into the last ring slot (free until chunk NR - 1), so the chunk waits
-  // cover it.
-  dma16_lds(a.q + b * a.q_sb + (int64_t)h * D + cq * 16, ring + (NR - 1) * 4096);
+  // cover it. (Counted as DPC copies: the waits below are in whole chunks.)
+#pragma unroll
+  for (int u = 0; u < DPC; ++u)
+    dma16_lds(a.q + b * a.q_sb + (int64_t)h * D + cq * 16, ring + (NR - 1) * SLOT + u * 1024);
 #pragma unroll
   for (int i = 0; i < NR - 1; ++i)
     if (i < T) issue(i);
 
   int32_t mx = -32768;
-  uint32_t accd = 0;
-  int32_t hs = 0;
+  uint32_t accd[DPC];
+#pragma unroll
+  for (int u = 0; u < DPC; ++u) accd[u] = 0;
+  int32_t hs[DPC];
+#pragma unroll
+  for (int u = 0; u < DPC; ++u) hs[u] = 0;
   int32_t inv = 0;
   bool any_hi = false;
   v4i qv = v4i{0, 0, 0, 0};
@@ -745,52 +773,65 @@ __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, con
     form_p();
   }
   for (int i = 0; i < T; ++i) {
-    wait_vm_upto<NR - 2>(min(NR - 2, T - 1 - i));
+    wait_vm_upto<NR - 2, DPC>(min(NR - 2, T - 1 - i));
     if (i == 0) {
-      qv = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * 4096 + wave * 1024 + lane * 16);
+      qv = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * SLOT + wave * WB + lane * 16);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // q is read before its slot refills
     }
-    const v4i x = *reinterpret_cast<const v4i *>(sRing + (i % NR) * 4096 + wave * 1024 + lane * 16);
+    v4i x[DPC];
+#pragma unroll
+    for (int u = 0; u < DPC; ++u)
+      x[u] = *reinterpret_cast<const v4i *>(sRing + (i % NR) * SLOT + wave * WB + u * 1024 + lane * 16);
     // the slot of chunk i - 1 is free: this wave read it last iteration
     if (i + NR - 1 < T) issue(i + NR - 1);
     if (i < nK) {
-      int32_t acc = __builtin_amdgcn_sdot4(qv[0], x[0], 0, false);
-      acc = __builtin_amdgcn_sdot4(qv[1], x[1], acc, false);
-      acc = __builtin_amdgcn_sdot4(qv[2], x[2], acc, false);
-      acc = __builtin_amdgcn_sdot4(qv[3], x[3], acc, false);
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      const int j = i * CH + kl;
-      if (j < Tk) {
-        const int32_t h16 = qk_requant16(acc, a.qk_m, a.qk_s);
-        if (cq == 0) sS[j] = (int16_t)h16;
-        mx = max(mx, h16);
+#pragma unroll
+      for (int u = 0; u < DPC; ++u) {
+        int32_t acc = __builtin_amdgcn_sdot4(qv[0], x[u][0], 0, false);
+        acc = __builtin_amdgcn_sdot4(qv[1], x[u][1], acc, false);
+        acc = __builtin_amdgcn_sdot4(qv[2], x[u][2], acc, false);
+        acc = __builtin_amdgcn_sdot4(qv[3], x[u][3], acc, false);
+        acc += __shfl_xor(acc, 1);
+        acc += __shfl_xor(acc, 2);
+        const int j = i * CH + kkey + 16 * u;
+        if (j < Tk) {
+          const int32_t h16 = qk_requant16(acc, a.qk_m, a.qk_s);
+          if (cq == 0) sS[j] = (int16_t)h16;
+          mx = max(mx, h16);
+        }
       }
       if (i == nK - 1) form_p();
     } else {
-      const uint4 pv = *reinterpret_cast<const uint4 *>(sP + (i - nK) * CH + cq * 16);
+      const uint4 pv = *reinterpret_cast<const uint4 *>(sP + (i - nK) * CH + vp * 16);
       const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
-      if (!any_hi) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) accd = (uint32_t)__builtin_amdgcn_sdot4((int)pw[e], x[e], (int)accd, false);
-      } else {
-        // P = 128 only after an int16 row-max wrap: split off the top bit
+      for (int u = 0; u < DPC; ++u) {
+        if (!any_hi) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          accd = (uint32_t)__builtin_amdgcn_sdot4((int)(pw[e] & 0x7f7f7f7fu), x[e], (int)accd, false);
-          hs = __builtin_amdgcn_sdot4((int)((pw[e] >> 7) & 0x01010101u), x[e], hs, false);
+          for (int e = 0; e < 4; ++e)
+            accd[u] = (uint32_t)__builtin_amdgcn_sdot4((int)pw[e], x[u][e], (int)accd[u], false);
+        } else {
+          // P = 128 only after an int16 row-max wrap: split off the top bit
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            accd[u] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw[e] & 0x7f7f7f7fu), x[u][e], (int)accd[u], false);
+            hs[u] = __builtin_amdgcn_sdot4((int)((pw[e] >> 7) & 0x01010101u), x[u][e], hs[u], false);
+          }
         }
       }
     }
   }
-  accd += (uint32_t)hs << 7;
-  accd += (uint32_t)__shfl_xor((int)accd, 1);
-  accd += (uint32_t)__shfl_xor((int)accd, 2);
-  if (cq == 0) {
-    int32_t y = rshift((int32_t)(accd * (uint32_t)inv), a.rsqrt_off);
-    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
-    y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
-    a.out[b * a.o_sb + (int64_t)h * D + kl] = (int8_t)clampi(y, -127, 127);
+#pragma unroll
+  for (int u = 0; u < DPC; ++u) {
+    uint32_t v = accd[u] + ((uint32_t)hs[u] << 7);
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) v += (uint32_t)__shfl_xor((int)v, o);
+    if (vp == 0) {
+      int32_t y = rshift((int32_t)(v * (uint32_t)inv), a.rsqrt_off);
+      y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+      y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+      a.out[b * a.o_sb + (int64_t)h * D + vrow + u * RPD] = (int8_t)clampi(y, -127, 127);
+    }
   }
 }
 
@@ -870,11 +911,12 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
     // (self-attention caches up to 512 positions get their own, smaller
     // instance, so profiles separate it from cross-attention)
     if (a.max_tk <= 512)
-      hipLaunchKernelGGL((attn_decode_stream_kernel<512, 8>), grid, dim3(256), 0, s, a, pos);
+      hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a, pos);
     else if (a.max_tk <= 2048)
-      hipLaunchKernelGGL((attn_decode_stream_kernel<2048, 8>), grid, dim3(256), 0, s, a, pos);
+      hipLaunchKernelGGL((attn_decode_stream_kernel<2048, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a, pos);
     else
-      hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, 8>), grid, dim3(256), 0, s, a, pos);
+      hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a,
+                         pos);
     return check_launch("attn_decode_stream_kernel");
   }
 #define IW_DC(D_, P_) hipLaunchKernelGGL((attn_decode_cache_kernel<D_, P_>), grid, dim3(256), 0, s, a, pos)

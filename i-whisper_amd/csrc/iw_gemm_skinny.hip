@@ -277,22 +277,27 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_lds_kernel(GemmArgs g, Skinny
 }
 
 // ---------------------------------------------------------------------------
-// M-split kernel: one 32-row m-subtile x 32 columns per block
+// M-split kernel: one 32-row m-subtile x 32 NS columns per block
 // ---------------------------------------------------------------------------
 //
-// For decode grids (tiles x m-subtiles up to a few CUs' worth) each block
-// takes one 32 x 32 output tile over all of K, so it copies 32 x K bytes of
-// A and 32 x K of B instead of M x K of A. Stage s (128 K bytes: 4 KB of A,
-// 4 KB of B) belongs to wave s % 4, which copies it into its own LDS ring,
-// reads its fragments back and runs its four MFMAs: the four waves are
-// independent pipelines with no barrier in the K loop. Their partial tiles
-// are added in LDS (the rings' space) at the end. The blocks of one column
-// tile share blockIdx % 8, i.e. one XCD, so its B rows come from HBM once.
-template <int EPI, bool GELU, bool SCATTER, int WST>
+// For decode grids each block takes one 32 x (32 NS) output tile over all of
+// K, so it copies 32 x K bytes of A and 32 NS x K of B instead of M x K of A.
+// Stage s (128 K bytes: 4 KB of A, 4 NS KB of B) belongs to wave s % 4, which
+// copies it into its own LDS ring, reads its fragments back and runs its MFMAs:
+// the four waves are independent pipelines with no barrier in the K loop.
+// Their partial tiles are added in LDS (the rings' space) at the end. The
+// blocks of one column tile share blockIdx % 8, i.e. one XCD, so its B rows
+// come from HBM once. NS = 2 halves the A bytes every column of a wide GEMM
+// costs (A is re-read once per column tile).
+template <int EPI, bool GELU, bool SCATTER, int WST, int NS>
 __global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, SkinnyScatter sc, int ms,
                                                                  int tiles) {
-  constexpr int STB = 8192;  // bytes per stage: A rows then B rows, 128 bytes each
-  constexpr int PLDM = 33;
+  constexpr int STB = 4096 * (1 + NS);  // bytes per stage: A rows then B rows, 128 bytes each
+  constexpr int CPB = 32 * NS;          // columns per block
+  constexpr int PLDM = CPB + 1;
+  constexpr int DMA_STAGE = 4 + 4 * NS;  // copies per stage
+  constexpr int RPT = CPB / 8;           // epilogue rows per thread
+  static_assert(4 * 32 * PLDM * 4 <= WST * 4 * STB, "partials must fit the rings");
   __shared__ __attribute__((aligned(1024))) int8_t sRing[4 * WST * STB];
   __shared__ int32_t sXs[4][32];
   __shared__ uint8_t sLut[16];
@@ -304,38 +309,41 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, Ski
   const int msub = (bid >> 3) % ms;
   if (tile >= tiles) return;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
-  const int n0 = tile * TN, m0 = msub * 32;
+  const int n0 = tile * CPB, m0 = msub * 32;
   const bool zp = g.wz != nullptr;
 
   // epilogue inputs, requested before the K loop: thread t serves column
-  // t % 32 and rows t / 32 + 8 j of the subtile
-  const int cl = tid & 31;
+  // t % CPB and rows t / CPB + (256 / CPB) j of the subtile
+  const int cl = tid % CPB;
   const int n = n0 + cl;
-  const int mr0 = tid >> 5;
+  const int mr0 = tid / CPB;
   uint32_t lutv = 0;
   if (GELU && tid < 16) lutv = g.lut[tid];
   const ColRaw craw = load_col_raw(g, min(n, N - 1));
-  int32_t resv[4];
+  int32_t resv[RPT];
   if (EPI == EPI_L32RES) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      resv[j] = g.res[(int64_t)min(m0 + mr0 + 8 * j, M - 1) * g.ldres + min(n, N - 1)];
+    for (int j = 0; j < RPT; ++j)
+      resv[j] = g.res[(int64_t)min(m0 + mr0 + (256 / CPB) * j, M - 1) * g.ldres + min(n, N - 1)];
   }
   int pos = 0;
   if (SCATTER) pos = *sc.pos;
 
-  // copy j of a stage (j < 4: A, else B) fills rows 8 (j % 4) .. +7 of its
-  // half; lane l writes row 8 (j % 4) + l / 8 at position l % 8, fetching
-  // chunk (l % 8) ^ swz8(row)
+  // copy j of a stage fills rows 8 (j % 4) .. +7 of A (j < 4) or rows
+  // 8 (j - 4) .. +7 of B; lane l writes row r = 8 (.) + l / 8 at position
+  // l % 8, fetching chunk (l % 8) ^ swz8(r)
   const int r8 = lane >> 3;
   const int8_t *ga[4];
-  const int8_t *gb[4];
+  const int8_t *gb[4 * NS];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 8 * j + r8;
-    const int c = ((lane & 7) ^ swz8(r)) * 16;
-    ga[j] = g.a + (int64_t)min(m0 + r, M - 1) * g.lda + c;
-    gb[j] = g.b + (int64_t)min(n0 + r, N - 1) * g.ldb + c;
+    ga[j] = g.a + (int64_t)min(m0 + r, M - 1) * g.lda + ((lane & 7) ^ swz8(r)) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < 4 * NS; ++j) {
+    const int r = 8 * j + r8;
+    gb[j] = g.b + (int64_t)min(n0 + r, N - 1) * g.ldb + ((lane & 7) ^ swz8(r)) * 16;
   }
   const uint32_t ring =
       __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sRing)) + wave * WST * STB;
@@ -347,7 +355,7 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, Ski
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(ga[j] + k0, dst + j * 1024);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(gb[j] + k0, dst + 4096 + j * 1024);
+    for (int j = 0; j < 4 * NS; ++j) dma16(gb[j] + k0, dst + 4096 + j * 1024);
   };
 #pragma unroll
   for (int t = 0; t < WST - 1; ++t)
@@ -355,34 +363,45 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, Ski
 
   const int sw = swz8(lane & 31);
   const int8_t *wr = sRing + wave * WST * STB + (lane & 31) * SK;
-  v16i acc, acc2;
+  // NS == 1: two accumulators so that consecutive MFMAs do not wait on each
+  // other; NS == 2: one per column subtile
+  v16i acc[2];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0;
+  for (int r = 0; r < 16; ++r) acc[0][r] = acc[1][r] = 0;
   int32_t xs = 0;
   for (int t = 0; t < mine; ++t) {
     // stage t has landed once the copies of at most min(WST - 2, mine - 1 - t)
     // later stages are outstanding
     const int later = min(WST - 2, mine - 1 - t);
     if (WST >= 4 && later >= 2)
-      wait_vmcnt<16>();
+      wait_vmcnt<2 * DMA_STAGE>();
     else if (later >= 1)
-      wait_vmcnt<8>();
+      wait_vmcnt<DMA_STAGE>();
     else
       wait_vmcnt<0>();
     const int8_t *pa = wr + (t % WST) * STB;
-    v4i fa[4], fb[4];
+    v4i fa[4], fb[NS][4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int p = ((2 * ks + (lane >> 5)) ^ sw) * 16;
       fa[ks] = *reinterpret_cast<const v4i *>(pa + p);
-      fb[ks] = *reinterpret_cast<const v4i *>(pa + 4096 + p);
+#pragma unroll
+      for (int q = 0; q < NS; ++q) fb[q][ks] = *reinterpret_cast<const v4i *>(pa + 4096 * (1 + q) + p);
     }
     // the slot of stage t - 1 is free: its fragments were consumed
     if (t + WST - 1 < mine) issue(t + WST - 1);
+    if (NS == 1) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ks += 2) {
-      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks], fb[ks], acc, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks + 1], fb[ks + 1], acc2, 0, 0, 0);
+      for (int ks = 0; ks < 4; ks += 2) {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks], fb[0][ks], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks + 1], fb[0][ks + 1], acc[1], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int q = 0; q < NS; ++q)
+          acc[q] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ks], fb[q][ks], acc[q], 0, 0, 0);
     }
     if (zp) {
 #pragma unroll
@@ -393,13 +412,20 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, Ski
     xs += __shfl_xor(xs, 32);
     if (lane < 32) sXs[wave][lane] = xs;
   }
-  // partial tiles into the (now idle) rings: [wave][row][PLDM]
+  // partial tiles into the (now idle) rings: [wave][row][PLDM]. 32x32 MFMA
+  // layout: lane l holds column l % 32, register r row (r/4)*8 + (l/32)*4 + r%4.
   __syncthreads();
   int32_t *part = reinterpret_cast<int32_t *>(sRing) + wave * 32 * PLDM;
 #pragma unroll
-  for (int r = 0; r < 16; ++r)
-    part[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * PLDM + (lane & 31)] =
-        (int32_t)((uint32_t)acc[r] + (uint32_t)acc2[r]);
+  for (int r = 0; r < 16; ++r) {
+    const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    if (NS == 1) {
+      part[row * PLDM + (lane & 31)] = (int32_t)((uint32_t)acc[0][r] + (uint32_t)acc[1][r]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < NS; ++q) part[row * PLDM + q * 32 + (lane & 31)] = acc[q][r];
+    }
+  }
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
   __syncthreads();
 
@@ -407,8 +433,8 @@ __global__ __launch_bounds__(LNT) void gemm_skinny_msplit_kernel(GemmArgs g, Ski
   const ColParams c = decode_col<EPI>(g, craw);
   const int32_t *ps = reinterpret_cast<const int32_t *>(sRing);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = mr0 + 8 * j;
+  for (int j = 0; j < RPT; ++j) {
+    const int r = mr0 + (256 / CPB) * j;
     const int m = m0 + r;
     if (m < M) {
       uint32_t a = 0;
@@ -526,14 +552,18 @@ int launch_skinny(const GemmArgs &g, const SkinnyScatter &sc, hipStream_t s) {
   if (tiles == 0 || g.M == 0) return 0;
   const int ms = (int)((g.M + 31) / 32);
   if (lds_eligible(g) && tiles * ms <= kMsplitMaxBlocks) {
-    // one 32 x 32 tile per block; blocks of a column tile share an XCD
-    const dim3 grid((unsigned)(((tiles + 7) / 8) * 8 * ms)), block(LNT);
+    // one 32 x 32 tile per block; the blocks of a column tile share an XCD.
+    // Up to one block per CU: a 4-stage ring per wave (128 KB of LDS); more:
+    // 2 stages, two blocks per CU. (64-column tiles, NS = 2, measured slower
+    // for N = 3840 and 5120 at M = 128.)
+    const dim3 block(LNT);
+    const dim3 grid((unsigned)(((tiles + 7) / 8) * 8 * ms));
     if (tiles * ms <= kDeepRingTiles)
-      hipLaunchKernelGGL((gemm_skinny_msplit_kernel<EPI, GELU, SCATTER, 4>), grid, block, 0, s, g, sc, ms,
-                         (int)tiles);
+      hipLaunchKernelGGL((gemm_skinny_msplit_kernel<EPI, GELU, SCATTER, 4, 1>), grid, block, 0, s, g, sc,
+                         ms, (int)tiles);
     else
-      hipLaunchKernelGGL((gemm_skinny_msplit_kernel<EPI, GELU, SCATTER, 2>), grid, block, 0, s, g, sc, ms,
-                         (int)tiles);
+      hipLaunchKernelGGL((gemm_skinny_msplit_kernel<EPI, GELU, SCATTER, 2, 1>), grid, block, 0, s, g, sc,
+                         ms, (int)tiles);
     return check_launch("gemm_skinny_msplit_kernel");
   }
   if (lds_eligible(g)) {
