@@ -618,18 +618,18 @@ int iw_greedy_advance(const int8_t *logits, int64_t rows, int64_t cols, int64_t 
                       int64_t *next_tokens, int64_t *history, int64_t history_ld,
                       int64_t history_cols, int32_t *step, int32_t *pos, int32_t pos_increment,
                       iw_stream_t stream) {
-  IW_REQUIRE(rows >= 0 && cols > 0 && ld >= cols && history_cols > 0 && history_ld >= history_cols,
-             "invalid greedy step shape");
+  IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 23) && ld >= cols && history_cols > 0 &&
+                 history_ld >= history_cols,
+             "invalid greedy step shape (at most 2^23 - 1 columns)");
   IW_REQUIRE(logits && next_tokens && history && step && pos, "null tensor pointer");
-  int rc = rows ? launch_argmax_rows(logits, rows, cols, ld, next_tokens, as_stream(stream)) : 0;
-  if (rc) return rc;
-  return launch_greedy_record(next_tokens, history, rows, history_ld, history_cols, step, pos,
-                              pos_increment, as_stream(stream));
+  return launch_greedy_step(logits, rows, cols, ld, next_tokens, history, history_ld, history_cols, step,
+                            pos, pos_increment, as_stream(stream));
 }
 
 int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                    iw_stream_t stream) {
-  IW_REQUIRE(rows >= 0 && cols > 0 && ld >= cols, "invalid argmax shape");
+  IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 23) && ld >= cols,
+             "invalid argmax shape (at most 2^23 - 1 columns)");
   if (rows == 0) return IW_OK;
   IW_REQUIRE(x && out, "null tensor pointer");
   return launch_argmax_rows(x, rows, cols, ld, out, as_stream(stream));

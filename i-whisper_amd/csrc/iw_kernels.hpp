@@ -48,9 +48,11 @@ int launch_add_requant15(const int8_t *x, const int64_t *tokens, const int8_t *a
                          const uint16_t *mult, const int8_t *shift, int16_t *out, int64_t batch,
                          int64_t positions, int64_t channels, int mpc, int spc, hipStream_t s,
                          const int32_t *pos = nullptr, int64_t addend_rows = 0);
-int launch_greedy_record(const int64_t *next, int64_t *history, int64_t rows, int64_t hist_ld,
-                         int64_t hist_cols, int32_t *step, int32_t *pos, int32_t pos_inc,
-                         hipStream_t s);
+// argmax of each logits row into next (and history[row][*step] when
+// *step < hist_cols), then *step += 1, *pos += pos_inc
+int launch_greedy_step(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t *next,
+                       int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
+                       int32_t *pos, int32_t pos_inc, hipStream_t s);
 int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, int64_t m,
                         int64_t t, hipStream_t s);
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,

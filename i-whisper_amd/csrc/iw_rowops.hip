@@ -140,6 +140,100 @@ __global__ __launch_bounds__(256) void layernorm32_kernel(
   }
 }
 
+// Wave-wide sum / max with DPP moves (no LDS round trips): xor-1 and xor-2
+// quad permutes, then the half-row and row mirrors give every lane its
+// 16-lane row's total; the four rows are added from lanes 0, 16, 32, 48.
+__device__ __forceinline__ uint32_t row16_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true);   // quad [1,0,3,2]
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true);   // quad [2,3,0,1]
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, true);  // row_half_mirror
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, true);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
+  v = row16_sum(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+}
+__device__ __forceinline__ int32_t wave_max_dpp(int32_t v) {
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0xB1, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x4E, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x141, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x140, 0xf, 0xf, false));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// LayerNorm32 for few rows (a decode step): one row per block of 256 threads,
+// thread t owning elements t, t + 256, ... so that each row's arithmetic is
+// spread over four SIMDs. Same integer steps as layernorm32_kernel.
+constexpr int LNR_MAX = 5;  // 1280 / 256
+__global__ __launch_bounds__(256) void layernorm32_row_kernel(
+    const int16_t *__restrict__ x, const int8_t *__restrict__ gamma,
+    const int32_t *__restrict__ beta, uint32_t ln_m, int32_t ln_s, uint32_t out_m,
+    int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int hidden, int code) {
+  __shared__ uint32_t sA[4], sB[4], sC[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int16_t *xr = x + row * hidden;
+  int32_t v[LNR_MAX], gm[LNR_MAX], bt[LNR_MAX];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < LNR_MAX; ++j) {
+    const int e = tid + 256 * j;
+    const bool ok = e < hidden;
+    v[j] = ok ? xr[e] : 0;
+    gm[j] = ok ? gamma[e] : 0;
+    bt[j] = (ok && beta) ? beta[e] : 0;
+    sum += (uint32_t)v[j];
+  }
+  sum = wave_sum_dpp(sum);
+  if (lane == 0) sA[wave] = sum;
+  __syncthreads();
+  const int32_t mean = norm_reduce((int32_t)(sA[0] + sA[1] + sA[2] + sA[3]), code);
+  int32_t maxsq = 0;
+#pragma unroll
+  for (int j = 0; j < LNR_MAX; ++j) {
+    if (tid + 256 * j < hidden) {
+      const int32_t d = v[j] - mean;
+      maxsq = max(maxsq, (int32_t)((uint32_t)d * (uint32_t)d));
+    }
+  }
+  maxsq = wave_max_dpp(maxsq);
+  if (lane == 0) sB[wave] = (uint32_t)maxsq;
+  __syncthreads();
+  maxsq = max(max((int32_t)sB[0], (int32_t)sB[1]), max((int32_t)sB[2], (int32_t)sB[3]));
+  int32_t rs = bitlen(maxsq) - 16;
+  rs = rs < 0 ? 0 : rs;
+  rs = (rs + 1) & ~1;
+  uint32_t vs = 0;
+#pragma unroll
+  for (int j = 0; j < LNR_MAX; ++j) {
+    if (tid + 256 * j < hidden) {
+      const int32_t d = v[j] - mean;
+      vs += (uint32_t)rshift((int32_t)((uint32_t)d * (uint32_t)d), (uint32_t)rs);
+    }
+  }
+  vs = wave_sum_dpp(vs);
+  if (lane == 0) sC[wave] = vs;
+  __syncthreads();
+  const int32_t var = norm_reduce((int32_t)(sC[0] + sC[1] + sC[2] + sC[3]), code);
+  const int32_t inv = fisr(var, rsqrt_off);
+  const uint32_t nshift = (uint32_t)(ln_s + (rs >> 1));
+  int8_t *orow = out + row * hidden;
+#pragma unroll
+  for (int j = 0; j < LNR_MAX; ++j) {
+    const int e = tid + 256 * j;
+    if (e < hidden) {
+      const int32_t d = v[j] - mean;
+      const uint32_t t = (uint32_t)d * (uint32_t)inv * ln_m;
+      const int32_t y = clampi(rshift((int32_t)t, nshift), -16383, 16383);
+      const uint32_t a = (uint32_t)y * (uint32_t)gm[j] + (uint32_t)bt[j];
+      orow[e] = (int8_t)clampi(rshift(mulh((int32_t)a, out_m), (uint32_t)out_s), -127, 127);
+    }
+  }
+}
+
 __global__ void rsqrt_kernel(const int32_t *x, int32_t *out, int64_t n, uint32_t off) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = fisr(x[i], off);
@@ -212,50 +306,70 @@ __global__ void quantize_mel_kernel(const float *__restrict__ mel, float alpha,
   }
 }
 
-// First index of the row maximum (torch.argmax tie rule) over int8 logits.
+// First index of the row maximum (torch.argmax tie rule) over int8 logits,
+// one block per row. The row is read in 16-byte pieces from its first
+// 16-byte boundary (the bytes before it and after the last whole piece one
+// at a time); each thread visits its indices in increasing order, keeping
+// the first maximum, and the block reduces keys (value + 128) << 23 |
+// (2^23 - 1 - index), whose maximum is the first maximal element. When
+// `step` is given, the index is also recorded in history[row][*step] (if
+// *step < hist_cols).
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const int8_t *__restrict__ x,
                                                           int64_t cols, int64_t ld,
-                                                          int64_t *__restrict__ out) {
+                                                          int64_t *__restrict__ out,
+                                                          int64_t *__restrict__ history,
+                                                          int64_t hist_ld, int64_t hist_cols,
+                                                          const int32_t *step) {
+  __shared__ int32_t sk[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   const int8_t *xr = x + row * ld;
-  int32_t best = -1000;
-  int64_t bi = 0;
-  for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-    const int32_t v = xr[c];
-    if (v > best) {
-      best = v;
-      bi = c;
-    }
+  const int n = (int)cols;
+  const int head = min((int)((16 - (reinterpret_cast<uintptr_t>(xr) & 15)) & 15), n);
+  const int pieces = (n - head) >> 4;
+  const int tail0 = head + (pieces << 4);
+  int32_t best = -1000, bi = 0;
+  if (tid < head) {
+    best = xr[tid];
+    bi = tid;
   }
-  __shared__ int32_t sv[256];
-  __shared__ int64_t si[256];
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      const int32_t ov = sv[threadIdx.x + s];
-      const int64_t oi = si[threadIdx.x + s];
-      if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
+  const uint4 *xa = reinterpret_cast<const uint4 *>(xr + head);
+  for (int c = tid; c < pieces; c += 256) {
+    const uint4 w = xa[c];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int32_t v = (int32_t)(int8_t)(ws[e >> 2] >> (8 * (e & 3)));
+      if (v > best) {
+        best = v;
+        bi = head + (c << 4) + e;
       }
     }
-    __syncthreads();
   }
-  if (threadIdx.x == 0) out[row] = si[0];
+  if (tail0 + tid < n) {
+    const int32_t v = xr[tail0 + tid];
+    if (v > best) {
+      best = v;
+      bi = tail0 + tid;
+    }
+  }
+  int32_t key = best < -128 ? 0 : (((best + 128) << 23) | (0x7FFFFF - bi));
+  key = wave_max_dpp(key);
+  if (lane == 0) sk[wave] = key;
+  __syncthreads();
+  if (tid == 0) {
+    key = max(max(sk[0], sk[1]), max(sk[2], sk[3]));
+    const int64_t idx = 0x7FFFFF - (key & 0x7FFFFF);
+    out[row] = idx;
+    if (history) {
+      const int32_t st = *step;
+      if (st >= 0 && st < hist_cols) history[row * hist_ld + st] = idx;
+    }
+  }
 }
 
 // Greedy step bookkeeping after argmax_rows wrote next[]: record the tokens
 // in column *step of the history and advance the device-side counters.
-__global__ void greedy_record_kernel(const int64_t *__restrict__ next, int64_t *__restrict__ history,
-                                     int64_t rows, int64_t hist_ld, int64_t hist_cols,
-                                     const int32_t *step) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int32_t st = *step;
-  if (r < rows && st >= 0 && st < hist_cols) history[r * hist_ld + st] = next[r];
-}
-
 __global__ void greedy_advance_kernel(int32_t *step, int32_t *pos, int32_t pos_inc) {
   if (threadIdx.x == 0) {
     *step += 1;
@@ -332,6 +446,9 @@ int grid_for(int64_t n, int threads) {
 
 }  // namespace
 
+// row counts up to which each row gets a block of its own
+constexpr int64_t kLnRowBlockMaxRows = 2048;
+
 int layernorm_width_code(int64_t h) {
   switch (h) {
     case 384: return 0;
@@ -349,11 +466,16 @@ int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *bet
   const int code = layernorm_width_code(hidden);
   if (code < 0) return fail("unsupported LayerNorm hidden size: " + std::to_string(hidden));
   if (rows == 0) return 0;
-  // one row per wave; few rows (a decode step) get a block each, so they
-  // spread over as many CUs as there are rows
-  const int per_block = rows >= 4096 ? 4 : 1;
-  const int64_t blocks = (rows + per_block - 1) / per_block;
-  hipLaunchKernelGGL(layernorm32_kernel, dim3((unsigned)blocks), dim3(64 * per_block), 0, s, x, gamma, beta,
+  if (rows <= kLnRowBlockMaxRows) {
+    // few rows (a decode step): a block of 256 threads per row
+    hipLaunchKernelGGL(layernorm32_row_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, gamma, beta,
+                       (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, (int)hidden,
+                       code);
+    return check_launch("layernorm32_row_kernel");
+  }
+  // one row per wave, four rows per block
+  const int64_t blocks = (rows + 3) / 4;
+  hipLaunchKernelGGL(layernorm32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, gamma, beta,
                      (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, rows,
                      (int)hidden, code);
   return check_launch("layernorm32_kernel");
@@ -433,13 +555,13 @@ int launch_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *
   return check_launch("copy_rows_kernel");
 }
 
-int launch_greedy_record(const int64_t *next, int64_t *history, int64_t rows, int64_t hist_ld,
-                         int64_t hist_cols, int32_t *step, int32_t *pos, int32_t pos_inc,
-                         hipStream_t s) {
+int launch_greedy_step(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t *next,
+                       int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
+                       int32_t *pos, int32_t pos_inc, hipStream_t s) {
   if (rows > 0) {
-    hipLaunchKernelGGL(greedy_record_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s,
-                       next, history, rows, hist_ld, hist_cols, step);
-    int rc = check_launch("greedy_record_kernel");
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols, ld, next,
+                       history, hist_ld, hist_cols, step);
+    int rc = check_launch("argmax_rows_kernel");
     if (rc) return rc;
   }
   hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(64), 0, s, step, pos, pos_inc);
@@ -449,7 +571,8 @@ int launch_greedy_record(const int64_t *next, int64_t *history, int64_t rows, in
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                        hipStream_t s) {
   if (rows == 0) return 0;
-  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, cols, ld, out);
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, cols, ld, out,
+                     (int64_t *)nullptr, (int64_t)0, (int64_t)0, (const int32_t *)nullptr);
   return check_launch("argmax_rows_kernel");
 }
 

@@ -386,3 +386,22 @@ def test_argmax_rows(iw, gpu):
     x[4, 200] = 127
     got = host(iw.kernels.argmax_rows_hip(T(x)))
     assert np.array_equal(got, np.argmax(x, axis=1))
+
+
+@pytest.mark.parametrize("cols", [1, 15, 16, 17, 40, 4099, 51865])
+def test_argmax_rows_ties_and_alignment(iw, gpu, cols):
+    """Rows starting at every offset mod 16 (odd row stride), maxima tied in the
+    unaligned head, the 16-byte pieces and the tail, and all-equal rows."""
+    r = gen.rng(cols)
+    rows = 19
+    x = gen.i8(r, (rows, cols))
+    x[0, :] = -128
+    x[1, :] = 7
+    for i in range(2, rows):
+        picks = r.integers(0, cols, size=min(3, cols))
+        x[i, picks] = 127
+    xt = T(x)  # row stride = cols: odd strides put row starts at every alignment
+    out = torch.empty(rows, dtype=torch.int64, device="cuda")
+    iw._lib.call("iw_argmax_rows", xt.data_ptr(), rows, cols, cols, out.data_ptr(),
+                 torch.cuda.current_stream().cuda_stream)
+    assert np.array_equal(host(out), np.argmax(x, axis=1))
