@@ -82,6 +82,8 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   constexpr int ACP = A_STAGE / 1024 / 4;   // A copies per wave per stage
   constexpr int BCP = B_STAGE / 1024 / 4;   // B copies per wave per stage
   constexpr int KS = BK / 32;               // k32 steps per stage
+  static_assert(KS % 2 == 0, "the fragment pipeline alternates two register sets");
+  static_assert(ACP + BCP <= 8, "copies of a stage are spread over one k32 step's MFMAs");
   // the operand ring; after the K loop it holds the output tile on its way
   // to row-contiguous stores
   __shared__ __attribute__((aligned(1024))) int8_t sMem[STAGES * (A_STAGE + B_STAGE)];
@@ -138,17 +140,24 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   const uint32_t ldsA = __builtin_amdgcn_readfirstlane(lds_addr(sA) + wave * ACP * 1024);
   const uint32_t ldsB = __builtin_amdgcn_readfirstlane(lds_addr(sB) + wave * BCP * 1024);
   const int nk = K / BK;
-  auto issue = [&](int kt) {
+  // copy c (A copies first, then B) of stage kt; stages past the end repeat
+  // the last tile (harmless: those slots are never read)
+  auto issue_one = [&](int kt, int c) {
     const int st = kt % STAGES;
-    const int k0 = min(kt, nk - 1) * BK;  // past the end: a harmless repeat of the last tile
+    const int k0 = min(kt, nk - 1) * BK;
+    if (c < ACP)
+      dma16(ga[c] + k0, ldsA + st * A_STAGE + c * 1024);
+    else
+      dma16(gb[c - ACP] + k0, ldsB + st * B_STAGE + (c - ACP) * 1024);
+  };
+  auto issue = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < ACP; ++i) dma16(ga[i] + k0, ldsA + st * A_STAGE + i * 1024);
-#pragma unroll
-    for (int i = 0; i < BCP; ++i) dma16(gb[i] + k0, ldsB + st * B_STAGE + i * 1024);
+    for (int c = 0; c < ACP + BCP; ++c) issue_one(kt, c);
   };
 
   issue(0);
   issue(1);
+  issue(2);
 
   v16i acc[4][2];
 #pragma unroll
@@ -170,32 +179,75 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   const int aoff = (wm * 128 + (lane & 31)) * BK;
   const int boff = (wn * 64 + (lane & 31)) * BK;
 
-  // One stage is issued every iteration (the last two repeat the last tile),
-  // so at the top of iteration kt exactly one later stage is outstanding.
+  auto read_frags = [&](int kt, int ks, v4i (&fa)[4], v4i (&fb)[2]) {
+    const int8_t *pa = &sA[(kt % STAGES) * A_STAGE + aoff + fo[ks]];
+    const int8_t *pb = &sB[(kt % STAGES) * B_STAGE + boff + fo[ks]];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const v4i *>(pa + i * 32 * BK);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const v4i *>(pb + j * 32 * BK);
+  };
+  // the MFMAs of one k32 step with stage kt's copies spread between them
+  // (ndma of them, one after each MFMA), so the address unit is fed evenly
+  auto mfmas_dma = [&](const v4i (&fa)[4], const v4i (&fb)[2], int kt, int ndma) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      acc[t >> 1][t & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[t & 1], fa[t >> 1], acc[t >> 1][t & 1], 0, 0, 0);
+      if (t < ndma) issue_one(kt, t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (zp) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[i] = sum16v(fa[i], xs[i]);
+    }
+  };
+  auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[2]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    if (zp) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[i] = sum16v(fa[i], xs[i]);
+    }
+  };
+
+  // Software pipeline: the fragments of the next k32 step are read from LDS
+  // while the MFMAs of the current one run. Stage kt+1 is waited for (own
+  // copies, then the barrier for everyone's) before its first fragments are
+  // read; after that barrier every wave holds stage kt in registers, so
+  // stage kt+3 is copied into stage kt's slot. Three stages are issued ahead
+  // of the loop, so at the wait of iteration kt stages kt+1 and kt+2 are
+  // outstanding; stages past the end repeat the last tile and the final
+  // look-ahead reads are discarded.
+  v4i fa0[4], fb0[2], fa1[4], fb1[2];
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (ACP + BCP)) : "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  read_frags(0, 0, fa0, fb0);
   for (int kt = 0; kt < nk; ++kt) {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ACP + BCP) : "memory");
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue(kt + 2);
-    const int8_t *pa = &sA[(kt % STAGES) * A_STAGE + aoff];
-    const int8_t *pb = &sB[(kt % STAGES) * B_STAGE + boff];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      v4i fa[4], fb[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const v4i *>(pa + i * 32 * BK + fo[ks]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const v4i *>(pb + j * 32 * BK + fo[ks]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
-      if (zp) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xs[i] = sum16v(fa[i], xs[i]);
+    for (int ks = 0; ks + 1 < KS; ks += 2) {
+      read_frags(kt, ks + 1, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(fa0, fb0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 2 < KS) {
+        read_frags(kt, ks + 2, fa0, fb0);
+      } else {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ACP + BCP) : "memory");
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        read_frags(kt + 1, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (ks + 2 < KS)
+        mfmas(fa1, fb1);
+      else
+        mfmas_dma(fa1, fb1, kt + 3, ACP + BCP);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated copies land before the ring is reused
