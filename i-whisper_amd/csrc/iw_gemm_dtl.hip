@@ -30,9 +30,14 @@ using namespace gemm;
 
 namespace {
 
-constexpr int BM = 256, BN = 128, STAGES = 3;
+// Waves along N; each wave owns 128 x 64 outputs. WN = 4 (256 x 256 tiles,
+// eight waves, one block per CU) moves a third fewer operand bytes per MFMA
+// than WN = 2 (256 x 128, two blocks per CU) and measured faster overall.
+constexpr int WN = 4;
+constexpr int NWAVES = 2 * WN;
+constexpr int BM = 256, BN = 64 * WN, STAGES = 3;
 
-constexpr int NT = 256;
+constexpr int NT = 64 * NWAVES;
 constexpr int XCDS = 8;
 
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): the wave
@@ -70,6 +75,47 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 1) & 2) | (((r >> 1) ^
 // 128-byte rows (8 chunks): chunk c of row r at position c ^ swz8(r)
 __device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
 
+// Round-half-away-from-zero right shift (the Shift rule) in three operations:
+// the sign term is a one-bit field extract whose width is 0 for a zero shift.
+struct EpiShift {
+  uint32_t half, sh, w;
+  __device__ __forceinline__ void set(uint32_t h, uint32_t s) { half = h, sh = s, w = min(s, 1u); }
+  __device__ __forceinline__ int32_t apply(uint32_t x) const {
+    const uint32_t sgn = (uint32_t)__builtin_amdgcn_sbfe((int32_t)x, 31, w);
+    return (int32_t)(x + half + sgn) >> sh;
+  }
+};
+
+// Per-column requantization operands for one output column.
+struct EpiCol {
+  int32_t m;      // multiplier as int32 (mneg restores the unsigned value)
+  uint32_t mneg;  // all ones when the multiplier is >= 2^31
+  uint32_t half, sh;
+  int32_t nz;     // negated zero point
+  uint32_t b;
+  __device__ __forceinline__ void set(uint32_t mult, uint32_t shift, uint32_t nzp, uint32_t bias) {
+    m = (int32_t)mult, mneg = (uint32_t)((int32_t)mult >> 31), sh = shift, nz = (int32_t)nzp, b = bias;
+  }
+  // acc - wz * rowsum + bias, modulo 2^32 (|wz * rowsum| < 2^31 for K <= 32768)
+  __device__ __forceinline__ uint32_t corrected(int32_t acc, int32_t xsum) const {
+    return (uint32_t)__mul24(nz, xsum) + (uint32_t)acc + b;
+  }
+  // high word of the signed x unsigned 64-bit product
+  __device__ __forceinline__ int32_t mulh(uint32_t x) const {
+    return (int32_t)((uint32_t)__mulhi((int32_t)x, m) + (x & mneg));
+  }
+  // Linear8 / per-tensor int8: clamp(rshift(mulh(corrected), s), -127, 127)
+  __device__ __forceinline__ int32_t requant8(int32_t acc, int32_t xsum) const {
+    const uint32_t hi = (uint32_t)mulh(corrected(acc, xsum));
+    const uint32_t sgn = (uint32_t)__builtin_amdgcn_sbfe((int32_t)hi, 31, min(sh, 1u));
+    return clampi((int32_t)(hi + half + sgn) >> sh, -127, 127);
+  }
+  // Linear32: mulh(corrected) << s
+  __device__ __forceinline__ uint32_t pre_residual(int32_t acc, int32_t xsum) const {
+    return (uint32_t)mulh(corrected(acc, xsum)) << sh;
+  }
+};
+
 // BK: K bytes per stage (64: 3 x 72 KB rings, two blocks per CU; 128: every
 // wave-wide copy reads 8 whole 128-byte lines instead of 16 half lines,
 // 3 x 144 KB, one block per CU)
@@ -79,8 +125,8 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   constexpr int A_STAGE = BM * BK, B_STAGE = BN * BK;
   constexpr int CPR = BK / 16;              // 16-byte chunks per LDS row
   constexpr int RPI = 64 / CPR;             // rows per wave-wide copy
-  constexpr int ACP = A_STAGE / 1024 / 4;   // A copies per wave per stage
-  constexpr int BCP = B_STAGE / 1024 / 4;   // B copies per wave per stage
+  constexpr int ACP = A_STAGE / 1024 / NWAVES;  // A copies per wave per stage
+  constexpr int BCP = B_STAGE / 1024 / NWAVES;  // B copies per wave per stage
   constexpr int KS = BK / 32;               // k32 steps per stage
   static_assert(KS % 2 == 0, "the fragment pipeline alternates two register sets");
   static_assert(ACP + BCP <= 8, "copies of a stage are spread over one k32 step's MFMAs");
@@ -90,10 +136,12 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   int8_t *const sA = sMem;
   int8_t *const sB = sMem + STAGES * A_STAGE;
   __shared__ __attribute__((aligned(16))) int32_t sXsum[BM];
-  // per-column epilogue parameters of the tile's BN columns (decoded)
-  __shared__ __attribute__((aligned(16))) uint32_t sPm[BN], sPwz[BN], sPb[BN];
+  // per-column epilogue parameters of the tile's BN columns, decoded into
+  // the operands the per-element arithmetic takes: multiplier, rounding
+  // half (0 for a zero shift), shift amount, negated zero point, bias
+  __shared__ __attribute__((aligned(16))) uint32_t sPm[BN], sPh[BN], sPnz[BN], sPb[BN];
   __shared__ __attribute__((aligned(16))) int32_t sPsh[BN];
-  __shared__ __attribute__((aligned(16))) uint32_t sPgim[BN], sPgom[BN];
+  __shared__ __attribute__((aligned(16))) uint32_t sPgim[BN], sPgih[BN], sPgom[BN], sPgoh[BN];
   __shared__ __attribute__((aligned(16))) int32_t sPgis[BN], sPgos[BN];
   __shared__ uint8_t sLut[16];
 
@@ -106,7 +154,7 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int M = (int)g.M, N = (int)g.N, K = (int)g.K;
   constexpr bool zp = ZP;  // weights with zero points: A row sums are needed
   // Per-column parameters (thread t < BN: column n0 + t) and the GeLU table
@@ -253,26 +301,28 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated copies land before the ring is reused
 
   if (zp) {
-    // the two waves of a row half publish two subtiles each
+    // the WN waves of a row half publish 4 / WN subtiles each
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const int32_t v = wn ? xs[2 + ii] : xs[ii];
+    for (int ii = 0; ii < 4 / WN; ++ii) {
+      const int i = wn * (4 / WN) + ii;
+      const int32_t v = i == 0 ? xs[0] : i == 1 ? xs[1] : i == 2 ? xs[2] : xs[3];
       const int32_t s = v + __shfl_xor(v, 32);
-      if (lane < 32) sXsum[wm * 128 + (wn * 2 + ii) * 32 + lane] = s;
+      if (lane < 32) sXsum[wm * 128 + i * 32 + lane] = s;
     }
   }
   if (tid < BN) {
-    // decoded once per column; the shifts are kept as amounts (rounding
-    // constants are rebuilt where they are used)
     const ColParams c = decode_col<EPI>(g, craw);
     sPm[tid] = c.mult;
+    sPh[tid] = c.shift.half;
     sPsh[tid] = (int32_t)c.shift.sh;
-    sPwz[tid] = c.wz;
+    sPnz[tid] = 0u - c.wz;
     sPb[tid] = c.bias;
     if (GELU) {
       sPgim[tid] = c.gi_m;
+      sPgih[tid] = c.gi_s.half;
       sPgis[tid] = (int32_t)c.gi_s.sh;
       sPgom[tid] = c.go_m;
+      sPgoh[tid] = c.go_s.half;
       sPgos[tid] = (int32_t)c.go_s.sh;
     }
   }
@@ -292,8 +342,9 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   constexpr int OB = (EPI == EPI_L8 || EPI == EPI_S8) ? 1 : (EPI == EPI_L32 ? 4 : 2);
   constexpr bool BYTES = OB == 1;  // staged values: int8 results, else int32 pre-residual
   constexpr int SROW = BYTES ? 64 + 16 : 256 + 16;  // staging row bytes (padded)
-  constexpr int HALVES = BYTES ? 1 : 2;             // int32 staging: 64 rows at a time
+  constexpr int HALVES = BYTES ? 1 : WN;            // int32 staging: 128 / WN rows at a time
   constexpr int SROWS = 128 / HALVES;
+  static_assert(NWAVES * SROWS * SROW <= STAGES * (A_STAGE + B_STAGE), "staging fits in the ring");
   int8_t *const stage = sMem + wave * SROWS * SROW;
   const int ldo = (int)g.ldc * OB;
   const __amdgpu_buffer_rsrc_t out_rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -336,60 +387,61 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
         const int cl = j * 32 + q * 8 + (lane >> 5) * 4;  // first of 4 columns, wave-local
         const int cw = wn * 64 + cl;                     // tile-local
         const uint4 pm = *reinterpret_cast<const uint4 *>(&sPm[cw]);
-        const int4 psh = *reinterpret_cast<const int4 *>(&sPsh[cw]);
-        const uint4 pwz = *reinterpret_cast<const uint4 *>(&sPwz[cw]);
+        const uint4 psh = *reinterpret_cast<const uint4 *>(&sPsh[cw]);
+        const uint4 pnz = *reinterpret_cast<const uint4 *>(&sPnz[cw]);
         const uint4 pb = *reinterpret_cast<const uint4 *>(&sPb[cw]);
-        const uint32_t mv[4] = {pm.x, pm.y, pm.z, pm.w};
-        const int32_t shv[4] = {psh.x, psh.y, psh.z, psh.w};
-        const uint32_t wzv[4] = {pwz.x, pwz.y, pwz.z, pwz.w};
-        const uint32_t bv[4] = {pb.x, pb.y, pb.z, pb.w};
-        ColParams cp[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          cp[e].wz = wzv[e];
-          cp[e].bias = bv[e];
-          cp[e].mult = mv[e];
-          cp[e].shift = make_shift((uint32_t)shv[e]);
-          cp[e].shift.sh = (uint32_t)shv[e];
+        EpiCol ec[4];
+        ec[0].set(pm.x, psh.x, pnz.x, pb.x);
+        ec[1].set(pm.y, psh.y, pnz.y, pb.y);
+        ec[2].set(pm.z, psh.z, pnz.z, pb.z);
+        ec[3].set(pm.w, psh.w, pnz.w, pb.w);
+        if (BYTES) {
+          const uint4 ph = *reinterpret_cast<const uint4 *>(&sPh[cw]);
+          ec[0].half = ph.x, ec[1].half = ph.y, ec[2].half = ph.z, ec[3].half = ph.w;
         }
+        EpiShift gi[4], go[4];
+        uint32_t gim[4], gom[4];
         if (GELU) {
-          const uint4 gim = *reinterpret_cast<const uint4 *>(&sPgim[cw]);
-          const int4 gis = *reinterpret_cast<const int4 *>(&sPgis[cw]);
-          const uint4 gom = *reinterpret_cast<const uint4 *>(&sPgom[cw]);
-          const int4 gos = *reinterpret_cast<const int4 *>(&sPgos[cw]);
-          const uint32_t gimv[4] = {gim.x, gim.y, gim.z, gim.w};
-          const int32_t gisv[4] = {gis.x, gis.y, gis.z, gis.w};
-          const uint32_t gomv[4] = {gom.x, gom.y, gom.z, gom.w};
-          const int32_t gosv[4] = {gos.x, gos.y, gos.z, gos.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            cp[e].gi_m = gimv[e];
-            cp[e].gi_s = make_shift((uint32_t)gisv[e]);
-            cp[e].go_m = gomv[e];
-            cp[e].go_s = make_shift((uint32_t)gosv[e]);
-          }
+          const uint4 a = *reinterpret_cast<const uint4 *>(&sPgim[cw]);
+          const uint4 b = *reinterpret_cast<const uint4 *>(&sPgih[cw]);
+          const uint4 c = *reinterpret_cast<const uint4 *>(&sPgis[cw]);
+          const uint4 d = *reinterpret_cast<const uint4 *>(&sPgom[cw]);
+          const uint4 e = *reinterpret_cast<const uint4 *>(&sPgoh[cw]);
+          const uint4 f = *reinterpret_cast<const uint4 *>(&sPgos[cw]);
+          gim[0] = a.x, gim[1] = a.y, gim[2] = a.z, gim[3] = a.w;
+          gom[0] = d.x, gom[1] = d.y, gom[2] = d.z, gom[3] = d.w;
+          gi[0].set(b.x, c.x), gi[1].set(b.y, c.y), gi[2].set(b.z, c.z), gi[3].set(b.w, c.w);
+          go[0].set(e.x, f.x), go[1].set(e.y, f.y), go[2].set(e.z, f.z), go[3].set(e.w, f.w);
         }
 #pragma unroll
         for (int ii = 0; ii < 4 / HALVES; ++ii) {
           const int i = hf * (4 / HALVES) + ii;
           const int srow = ii * 32 + (lane & 31);  // staging row
           if (BYTES) {
-            uint32_t packed = 0;
+            int32_t y[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int32_t a = (int32_t)corrected_k32k(acc[i][j][q * 4 + e], xsm[i], cp[e]);
-              int32_t y = clampi(apply_shift(mulh_su(a, cp[e].mult), cp[e].shift), -127, 127);
-              if (GELU) y = gelu_dec(y, sLut, cp[e]);
-              packed |= (uint32_t)(uint8_t)y << (8 * e);
+            for (int e = 0; e < 4; ++e) y[e] = ec[e].requant8(acc[i][j][q * 4 + e], xsm[i]);
+            if (GELU) {
+              int32_t t[4];
+              uint8_t lv[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                t[e] = min(max(gi[e].apply((uint32_t)__mul24(y[e], (int32_t)gim[e])), -8), 7);
+                lv[e] = sLut[t[e] + 8];
+              }
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                y[e] = clampi(go[e].apply((uint32_t)__mul24(__mul24(y[e], (int32_t)lv[e]), (int32_t)gom[e])), -127, 127);
             }
+            // bytes y0..y3 (selector 0x0c gives a zero byte)
+            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)y[1], (uint32_t)y[0], 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)y[3], (uint32_t)y[2], 0x0c0c0400u);
+            const uint32_t packed = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
             *reinterpret_cast<uint32_t *>(stage + srow * SROW + cl) = packed;
           } else {
             uint32_t br[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int32_t a = (int32_t)corrected_k32k(acc[i][j][q * 4 + e], xsm[i], cp[e]);
-              br[e] = (uint32_t)mulh_su(a, cp[e].mult) << cp[e].shift.sh;
-            }
+            for (int e = 0; e < 4; ++e) br[e] = ec[e].pre_residual(acc[i][j][q * 4 + e], xsm[i]);
             *reinterpret_cast<uint4 *>(stage + srow * SROW + cl * 4) = make_uint4(br[0], br[1], br[2], br[3]);
           }
         }
