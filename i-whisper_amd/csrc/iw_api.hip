@@ -626,6 +626,24 @@ int iw_greedy_advance(const int8_t *logits, int64_t rows, int64_t cols, int64_t 
                             pos, pos_increment, as_stream(stream));
 }
 
+int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld,
+                               int64_t *next_tokens, int64_t *history, int64_t history_ld,
+                               int64_t history_cols, int32_t *step, int32_t *pos,
+                               int32_t pos_increment, const uint32_t *suppress,
+                               const uint32_t *suppress_first, const int64_t *prev0, int32_t eot,
+                               int32_t timestamp_begin, int32_t max_initial_timestamp,
+                               float logit_scale, iw_stream_t stream) {
+  IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 23) && ld >= cols && history_cols > 0 &&
+                 history_ld >= history_cols,
+             "invalid greedy step shape (at most 2^23 - 1 columns)");
+  IW_REQUIRE(logits && next_tokens && history && step && pos, "null tensor pointer");
+  IW_REQUIRE(timestamp_begin < 0 || eot >= 0, "the timestamp rules need the EOT id");
+  IW_REQUIRE(timestamp_begin < 0 || logit_scale > 0.f, "logit_scale must be positive");
+  return launch_greedy_step_filtered(logits, rows, cols, ld, next_tokens, history, history_ld, history_cols,
+                                     step, pos, pos_increment, suppress, suppress_first, prev0, eot,
+                                     timestamp_begin, max_initial_timestamp, logit_scale, as_stream(stream));
+}
+
 int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                    iw_stream_t stream) {
   IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 23) && ld >= cols,

@@ -55,6 +55,11 @@ int launch_greedy_step(const int8_t *logits, int64_t rows, int64_t cols, int64_t
                        int32_t *pos, int32_t pos_inc, hipStream_t s);
 int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, int64_t m,
                         int64_t t, hipStream_t s);
+int launch_greedy_step_filtered(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t *next,
+                                int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
+                                int32_t *pos, int32_t pos_inc, const uint32_t *mask, const uint32_t *mask_first,
+                                const int64_t *prev0, int32_t eot, int32_t ts_begin, int32_t max_init,
+                                float scale, hipStream_t s);
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                        hipStream_t s);
 int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,

@@ -368,6 +368,151 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const int8_t *__restri
   }
 }
 
+// Greedy token choice with the reference's logit filters applied on the
+// device (decoding.py:410-509 and GreedyDecoder.update, :275-296), one block
+// per row. The filters only remove candidates, so the argmax runs over the
+// allowed set of the int8 logits directly:
+//  * point masks (SuppressTokens, plus SuppressBlank's ids on the first
+//    sampled step and <|notimestamps|> under the timestamp rules) come as
+//    bitmasks over the vocabulary;
+//  * the timestamp rules (ApplyTimestampRules) leave the allowed set as
+//    [text_lo, ts_begin) + [ts_lo, ts_hi), derived from the sampled tokens
+//    history[row][0 .. *step);
+//  * their last rule ("sample a timestamp if the timestamp tokens' total
+//    probability exceeds every text token's") compares, in fp32 over the
+//    dequantised logits, logsumexp over the allowed timestamps with the
+//    largest allowed text logit (the log-softmax normaliser cancels);
+//  * a sequence whose previous token is EOT keeps emitting EOT.
+// With nothing allowed the result is index 0 (torch.argmax over all -inf).
+struct GreedyFilter {
+  const uint32_t *mask;        // suppressed at every step, or null
+  const uint32_t *mask_first;  // suppressed at the first sampled step, or null
+  const int64_t *prev0;        // per row: the token before the first sampled one, or null
+  int32_t eot;                 // < 0: no EOT freeze and no timestamp rules
+  int32_t ts_begin;            // < 0: no timestamp rules
+  int32_t max_init;            // max_initial_timestamp_index, < 0: none
+  float scale;                 // logit dequantisation scale (> 0)
+};
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+  return v;
+}
+
+__global__ __launch_bounds__(256) void greedy_filtered_kernel(const int8_t *__restrict__ x, int64_t cols,
+                                                              int64_t ld, int64_t *__restrict__ out,
+                                                              int64_t *__restrict__ history, int64_t hist_ld,
+                                                              int64_t hist_cols, const int32_t *step,
+                                                              GreedyFilter f) {
+  __shared__ uint32_t s_kt[4], s_ks[4];
+  __shared__ int32_t s_m[4], s_i[4];
+  __shared__ float s_s[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int n = (int)cols;
+  const int st = *step;
+  const int64_t *h = history + row * hist_ld;
+  const int nh = min(st, (int)hist_cols);  // sampled tokens held in the history
+
+  // ---- allowed set ----
+  int text_lo = 0, ts_b = n, ts_lo = n, ts_hi = n;
+  const bool rules = f.eot >= 0 && f.ts_begin >= 0;
+  if (rules) {
+    ts_b = min(f.ts_begin, n);
+    ts_lo = ts_b;
+    const int64_t last = nh >= 1 ? h[nh - 1] : -1, pen = nh >= 2 ? h[nh - 2] : -1;
+    const bool last_ts = nh >= 1 && last >= f.ts_begin;
+    const bool pen_ts = nh < 2 || pen >= f.ts_begin;
+    if (last_ts) {
+      if (pen_ts)
+        ts_hi = ts_lo;  // has to be a non-timestamp
+      else
+        text_lo = min(max(f.eot, 0), ts_b);  // cannot be normal text
+    }
+    // the last timestamp sampled so far
+    int im = -1;
+    for (int i = tid; i < nh; i += 256)
+      if (h[i] >= f.ts_begin) im = i;
+    im = wave_max_i32(im);
+    if (lane == 0) s_i[wave] = im;
+    __syncthreads();
+    im = max(max(s_i[0], s_i[1]), max(s_i[2], s_i[3]));
+    if (im >= 0) {
+      const int64_t tl = h[im] + ((last_ts && !pen_ts) ? 0 : 1);  // non-decreasing, nonzero segments
+      ts_lo = (int)min(max((int64_t)ts_lo, tl), (int64_t)n);
+    }
+    if (nh == 0) {
+      text_lo = ts_b;  // the first sampled token is a timestamp
+      if (f.max_init >= 0) ts_hi = (int)min((int64_t)ts_hi, (int64_t)f.ts_begin + f.max_init + 1);
+    }
+    ts_hi = max(ts_hi, ts_lo);
+  }
+  const uint32_t *mk = (st == 0 && f.mask_first) ? f.mask_first : f.mask;
+  const int nw = (n + 31) >> 5;
+
+  // ---- one pass: text argmax key, timestamp argmax key, timestamp (max, sum exp) ----
+  uint32_t kt = 0, ks = 0;
+  int32_t m = -1000;
+  float sum = 0.f;
+  const int8_t *xr = x + row * ld;
+  for (int i0 = tid * 16; i0 < n; i0 += 256 * 16) {
+    uint32_t bits = 0;
+    if (mk) {
+      const int w = i0 >> 5, sh = i0 & 31;
+      uint64_t pair = mk[w];
+      if (w + 1 < nw) pair |= (uint64_t)mk[w + 1] << 32;
+      bits = (uint32_t)(pair >> sh) & 0xffffu;
+    }
+#pragma unroll 4
+    for (int e = 0; e < 16; ++e) {
+      const int i = i0 + e;
+      if (i >= n || ((bits >> e) & 1)) continue;
+      const int32_t v = xr[i];
+      const uint32_t key = ((uint32_t)(v + 129) << 23) | (uint32_t)(0x7FFFFF - i);
+      if (i >= text_lo && i < ts_b) {
+        kt = max(kt, key);
+      } else if (i >= ts_lo && i < ts_hi) {
+        ks = max(ks, key);
+        if (v > m) {
+          sum = sum * expf((float)(m - v) * f.scale) + 1.f;
+          m = v;
+        } else {
+          sum += expf((float)(v - m) * f.scale);
+        }
+      }
+    }
+  }
+  kt = wave_max_u32(kt);
+  ks = wave_max_u32(ks);
+  int32_t mw = wave_max_i32(m);
+  float sw = sum * expf((float)(m - mw) * f.scale);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sw += __shfl_xor(sw, o);
+  if (lane == 0) s_kt[wave] = kt, s_ks[wave] = ks, s_m[wave] = mw, s_s[wave] = sw;
+  __syncthreads();
+  if (tid == 0) {
+    kt = max(max(s_kt[0], s_kt[1]), max(s_kt[2], s_kt[3]));
+    ks = max(max(s_ks[0], s_ks[1]), max(s_ks[2], s_ks[3]));
+    uint32_t key = max(kt, ks);
+    if (rules && ks != 0) {
+      const int32_t mt = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
+      float st_sum = 0.f;
+      for (int w = 0; w < 4; ++w) st_sum += s_s[w] * expf((float)(s_m[w] - mt) * f.scale);
+      const float lse_ts = (float)mt * f.scale + logf(st_sum);
+      const bool ts_wins = kt == 0 || lse_ts > (float)((int32_t)(kt >> 23) - 129) * f.scale;
+      if (ts_wins) key = ks;
+    }
+    int64_t idx = key == 0 ? 0 : (int64_t)(0x7FFFFF - (key & 0x7FFFFF));
+    if (f.eot >= 0) {
+      const int64_t prev = nh >= 1 ? h[nh - 1] : (f.prev0 ? f.prev0[row] : -1);
+      if (prev == f.eot) idx = f.eot;
+    }
+    out[row] = idx;
+    if (st >= 0 && st < hist_cols) history[row * hist_ld + st] = idx;
+  }
+}
+
 // Greedy step bookkeeping after argmax_rows wrote next[]: record the tokens
 // in column *step of the history and advance the device-side counters.
 __global__ void greedy_advance_kernel(int32_t *step, int32_t *pos, int32_t pos_inc) {
@@ -562,6 +707,22 @@ int launch_greedy_step(const int8_t *logits, int64_t rows, int64_t cols, int64_t
     hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols, ld, next,
                        history, hist_ld, hist_cols, step);
     int rc = check_launch("argmax_rows_kernel");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(64), 0, s, step, pos, pos_inc);
+  return check_launch("greedy_advance_kernel");
+}
+
+int launch_greedy_step_filtered(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t *next,
+                                int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
+                                int32_t *pos, int32_t pos_inc, const uint32_t *mask, const uint32_t *mask_first,
+                                const int64_t *prev0, int32_t eot, int32_t ts_begin, int32_t max_init,
+                                float scale, hipStream_t s) {
+  if (rows > 0) {
+    const GreedyFilter f{mask, mask_first, prev0, eot, ts_begin, max_init, scale};
+    hipLaunchKernelGGL(greedy_filtered_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols, ld, next,
+                       history, hist_ld, hist_cols, step, f);
+    int rc = check_launch("greedy_filtered_kernel");
     if (rc) return rc;
   }
   hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(64), 0, s, step, pos, pos_inc);

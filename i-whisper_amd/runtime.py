@@ -18,8 +18,10 @@ chosen for the MI355X instead of the reference's per-call tensors:
 """
 from __future__ import annotations
 
-from typing import List, Optional
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -166,6 +168,37 @@ class EncoderRunner:
         return self.out
 
 
+@dataclass
+class LogitFilters:
+    """The decoding task's logit filters (decoding.py:410-509, built as in
+    DecodingTask, :556-572) and the EOT freeze of GreedyDecoder.update
+    (:290), applied on the device inside the greedy step.
+
+    ``suppress_tokens``: SuppressTokens ids; ``suppress_blank``: SuppressBlank
+    ids (``tokenizer.encode(" ") + [eot]``), empty = no SuppressBlank;
+    ``timestamp_begin`` >= 0 turns ApplyTimestampRules on, with
+    ``no_timestamps`` and ``max_initial_timestamp_index`` (< 0 = None) and the
+    logits' dequantisation scale ``logit_scale`` (None = the decoder's
+    1 / act_logits_alpha)."""
+    eot: int
+    suppress_tokens: Sequence[int] = ()
+    suppress_blank: Sequence[int] = ()
+    timestamp_begin: int = -1
+    no_timestamps: int = -1
+    max_initial_timestamp_index: int = -1
+    logit_scale: Optional[float] = None
+
+
+def _bitmask(ids, n: int, dev) -> torch.Tensor:
+    words = np.zeros((n + 31) // 32, np.uint32)
+    for i in ids:
+        i = int(i)
+        if not 0 <= i < n:
+            raise ValueError(f"token id {i} outside the vocabulary")
+        words[i >> 5] |= np.uint32(1) << np.uint32(i & 31)
+    return torch.from_numpy(words).to(dev)
+
+
 class DecoderRunner:
     """Greedy TextDecoder_int steps over preallocated self/cross KV caches.
 
@@ -179,7 +212,8 @@ class DecoderRunner:
     """
 
     def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int,
-                 max_steps: Optional[int] = None, use_graph: bool = True):
+                 max_steps: Optional[int] = None, use_graph: bool = True,
+                 filters: Optional[LogitFilters] = None):
         self.dec = decoder
         self.B = batch
         C, H = decoder.n_state, decoder.n_head
@@ -216,6 +250,22 @@ class DecoderRunner:
         self.history = torch.zeros((batch, self.hist_cols), dtype=torch.int64, device=dev)
         self.graph = None
         self.graph_stream = None
+        self.prev0 = torch.zeros(batch, dtype=torch.int64, device=dev)  # the prompt's last token
+        self.filters = filters
+        if filters is not None:
+            V = decoder.n_vocab
+            ts_on = filters.timestamp_begin >= 0
+            always = list(filters.suppress_tokens) + ([filters.no_timestamps]
+                                                       if ts_on and filters.no_timestamps >= 0 else [])
+            self.f_mask = _bitmask(always, V, dev) if always else None
+            self.f_first = _bitmask(always + list(filters.suppress_blank), V, dev) \
+                if filters.suppress_blank else None
+            scale = filters.logit_scale
+            if scale is None:
+                scale = 1.0 / float(decoder.act_logits_alpha.detach().reshape(-1)[0].item())
+            if ts_on and not scale > 0:
+                raise ValueError("the timestamp rules need a positive logit scale")
+            self.f_scale = float(scale)
 
     # ---- per utterance ----
     def set_audio(self, xa: torch.Tensor):
@@ -264,9 +314,17 @@ class DecoderRunner:
         _ln(dec.ln, x_last, self.B, self.h8)
         _lib.call("iw_classifier", self.h8.data_ptr(), dec.token_embedding.weight.data_ptr(), sc["cm"],
                   sc["cs"], self.logits.data_ptr(), self.B, self.C, dec.n_vocab, _stream())
-        _lib.call("iw_greedy_advance", self.logits.data_ptr(), self.B, dec.n_vocab, dec.n_vocab,
-                  self.tokens.data_ptr(), self.history.data_ptr(), self.hist_cols, self.hist_cols,
-                  self.step_no.data_ptr(), self.pos.data_ptr(), pos_inc, _stream())
+        f = self.filters
+        if f is None:
+            _lib.call("iw_greedy_advance", self.logits.data_ptr(), self.B, dec.n_vocab, dec.n_vocab,
+                      self.tokens.data_ptr(), self.history.data_ptr(), self.hist_cols, self.hist_cols,
+                      self.step_no.data_ptr(), self.pos.data_ptr(), pos_inc, _stream())
+        else:
+            _lib.call("iw_greedy_advance_filtered", self.logits.data_ptr(), self.B, dec.n_vocab,
+                      dec.n_vocab, self.tokens.data_ptr(), self.history.data_ptr(), self.hist_cols,
+                      self.hist_cols, self.step_no.data_ptr(), self.pos.data_ptr(), pos_inc,
+                      _ptr(self.f_mask), _ptr(self.f_first), self.prev0.data_ptr(), f.eot,
+                      f.timestamp_begin, f.max_initial_timestamp_index, self.f_scale, _stream())
 
     # ---- the prompt (several tokens, cache empty) ----
     def prompt_step(self, tokens: torch.Tensor):
@@ -372,6 +430,7 @@ class DecoderRunner:
         if steps > self.hist_cols:
             raise ValueError("more steps than the history holds")
         self.reset()
+        self.prev0.copy_(prompt[:, -1])
         logits = []
         self.prompt_step(prompt.contiguous())
         if keep_logits:
@@ -389,9 +448,11 @@ class DecoderRunner:
 
 def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torch.Tensor,
                   steps: int, runner: Optional[DecoderRunner] = None,
-                  keep_logits: bool = False):
+                  keep_logits: bool = False, filters: Optional[LogitFilters] = None):
     """Fixed-step greedy decoding; returns int64 tokens [B, prompt_len + steps] (and the int8
-    logits of every step [B, steps, vocab] when ``keep_logits``)."""
+    logits of every step [B, steps, vocab] when ``keep_logits``). With ``filters`` the decoding
+    task's logit filters and the EOT freeze apply at every step on the device; without them the
+    choice is the plain first-index argmax."""
     B, P = prompt.shape
     dec = model.decoder
     if P + steps > dec.n_ctx:
@@ -401,7 +462,10 @@ def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torc
     if steps <= 0:
         return prompt.clone()
     if runner is None:
-        runner = DecoderRunner(dec, B, audio_features.shape[1], use_graph=not keep_logits)
+        runner = DecoderRunner(dec, B, audio_features.shape[1], use_graph=not keep_logits,
+                               filters=filters)
+    elif filters is not None and runner.filters is not filters:
+        raise ValueError("the runner was built with other logit filters")
     runner.set_audio(audio_features)
     res = runner.run(prompt, steps, keep_logits=keep_logits)
     if keep_logits:

@@ -290,6 +290,36 @@ int iw_greedy_advance(const int8_t *logits, int64_t rows, int64_t cols, int64_t 
                       int64_t history_cols, int32_t *step, int32_t *pos, int32_t pos_increment,
                       iw_stream_t stream);
 
+/* The greedy step with the decoding task's logit filters applied on the
+ * device (decoding.py:410-509: SuppressBlank, SuppressTokens,
+ * ApplyTimestampRules; GreedyDecoder.update :275-296 for the EOT freeze),
+ * replacing the host-side filter loop of decoding.py:698-701. history[r][0 ..
+ * *step) holds the tokens sampled so far (column 0 is the first token after
+ * the prompt, i.e. sample_begin). Arguments after pos_increment:
+ *   suppress        bitmask, bit i of word i/32 set = token i suppressed at
+ *                   every step (SuppressTokens ids, and <|notimestamps|> when
+ *                   the timestamp rules are on); (cols + 31)/32 words; or NULL
+ *   suppress_first  the same for the first sampled step (adds SuppressBlank's
+ *                   " " and EOT); NULL = suppress
+ *   prev0           [rows] the token before the first sampled one (the
+ *                   prompt's last); NULL = none
+ *   eot             EOT id: rows whose previous token is EOT emit EOT; < 0
+ *                   disables this and the timestamp rules
+ *   timestamp_begin first timestamp id; < 0 disables the timestamp rules
+ *   max_initial_timestamp  max_initial_timestamp_index, < 0 = none
+ *   logit_scale     the logits' dequantisation scale (> 0), for the rule that
+ *                   compares logsumexp over timestamps with the best text
+ *                   logit in fp32
+ * All-suppressed rows give token 0 (torch.argmax over -inf). Then as
+ * iw_greedy_advance: history[r][*step] = next, *step += 1, *pos += pos_increment. */
+int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld,
+                               int64_t *next_tokens, int64_t *history, int64_t history_ld,
+                               int64_t history_cols, int32_t *step, int32_t *pos,
+                               int32_t pos_increment, const uint32_t *suppress,
+                               const uint32_t *suppress_first, const int64_t *prev0, int32_t eot,
+                               int32_t timestamp_begin, int32_t max_initial_timestamp,
+                               float logit_scale, iw_stream_t stream);
+
 /* Per-head gather into a [b][h][t][d] cache (the cross-attention K of
  * model_int.py:722-730, computed once per utterance):
  * dst[b*dst_sb + h*dst_sh + (t_offset+t)*dst_st + d] = src[b*src_sb + t*src_st + h*D + d]. */
