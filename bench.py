@@ -19,7 +19,9 @@ bounded sample on the host:
   WRITE_SIZE counters, scaled by the same counters on a plain copy, as
   recorded in profiles/attn_decode_cross_b128_pmc.md.
 * ``roofline_encoder_gemm``: the encoder GEMMs (int8 MFMA), HIP events around
-  every encoder GEMM launch in the timed steps.
+  every encoder GEMM launch in the timed steps. ``traffic`` is the layer
+  average of the same counters over the QKV, out-projection, FC1 and FC2
+  launches (profiles/encoder_gemm_large_b128_pmc.md).
 """
 from __future__ import annotations
 
@@ -90,21 +92,24 @@ def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: i
     }
 
 
-PMC_SUMMARY = ROOT / "profiles" / "attn_decode_cross_b128_pmc.md"
+PMC_SUMMARIES = (ROOT / "profiles" / "attn_decode_cross_b128_pmc.md",
+                 ROOT / "profiles" / "encoder_gemm_large_b128_pmc.md")
+GEMM_TRAFFIC_KEY = "gemm_dtl_kernel (encoder layer average)"
 # the decoder cross-attention kernel as profilers name it (key capacity, ring
 # slots, keys per chunk)
 XA_KERNEL = "attn_decode_stream_kernel<2048, 3, 128>"
 
 
 def recorded_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    """HBM bytes per launch of ``kernel`` from the committed counter summaries
     (a line ``traffic_bytes_per_launch <kernel>: <bytes>``), or None."""
-    try:
-        for line in PMC_SUMMARY.read_text().splitlines():
-            if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
-                return float(line.split(":")[1])
-    except OSError:
-        pass
+    for path in PMC_SUMMARIES:
+        try:
+            for line in path.read_text().splitlines():
+                if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                    return float(line.rsplit(":", 1)[1])
+        except OSError:
+            pass
     return None
 
 
@@ -233,7 +238,7 @@ def main():
         "roofline_encoder_gemm": {
             "bound": "mfma", "kernel": "gemm_dtl_kernel (encoder QKV/out/FC1/FC2 launches)",
             "achieved": round(g_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-            "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+            "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": recorded_traffic(GEMM_TRAFFIC_KEY),
             "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4)},
     }
     if dsteps:
