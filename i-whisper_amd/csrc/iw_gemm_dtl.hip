@@ -35,6 +35,7 @@ namespace {
 // than WN = 2 (256 x 128, two blocks per CU) and measured faster overall.
 constexpr int WN = 4;
 constexpr int NWAVES = 2 * WN;
+// three ring stages (96 KB); a fourth (128 KB) measured no faster
 constexpr int BM = 256, BN = 64 * WN, STAGES = 3;
 
 constexpr int NT = 64 * NWAVES;
@@ -216,10 +217,10 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   // copies of a stage are issued in two halves, H1 (copies [0, NC1)) and
   // H2 (the rest), one k32 step apart
   constexpr int NC = ACP + BCP, NC1 = NC / 2;
-  issue(0);
-  issue(1);
 #pragma unroll
-  for (int c = 0; c < NC1; ++c) issue_one(2, c);
+  for (int st = 0; st + 1 < STAGES; ++st) issue(st);
+#pragma unroll
+  for (int c = 0; c < NC1; ++c) issue_one(STAGES - 1, c);
 
   v16i acc[4][2];
 #pragma unroll
@@ -228,9 +229,21 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-  // row sums of the four m-subtiles' A fragments (each wave keeps the two
-  // its column half publishes; summing all four keeps the loop branch-free)
-  int32_t xs[4] = {0, 0, 0, 0};
+  // Row sums of the A fragments for the zero-point term: the WN waves of a
+  // row half share the same A rows, so wave wn sums only m-subtile wn (a
+  // wave-uniform choice, a scalar branch) and publishes it.
+  static_assert(WN == 4, "one m-subtile row sum per wave of a row half");
+  int32_t xs = 0;
+  auto rowsum = [&](const v4i (&fa)[4]) {
+    if (wn == 0)
+      xs = sum16v(fa[0], xs);
+    else if (wn == 1)
+      xs = sum16v(fa[1], xs);
+    else if (wn == 2)
+      xs = sum16v(fa[2], xs);
+    else
+      xs = sum16v(fa[3], xs);
+  };
 
   // Fragment reads: lane l reads row l % 32 of a 32-row subtile, chunk
   // 2*ks + l/32; the swizzle depends only on l % 32.
@@ -260,10 +273,7 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
       if (n > 0 && t % (8 / n) == 1 && t / (8 / n) < n) issue_one(kt, c0 + t / (8 / n));
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (zp) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xs[i] = sum16v(fa[i], xs[i]);
-    }
+    if (zp) rowsum(fa);
   };
   auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[2]) {
 #pragma unroll
@@ -271,22 +281,20 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
-    if (zp) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xs[i] = sum16v(fa[i], xs[i]);
-    }
+    if (zp) rowsum(fa);
   };
 
   // Software pipeline: the fragments of the next k32 step are read from LDS
   // while the MFMAs of the current one run. Stage kt+1 is waited for (own
   // copies, then the barrier for everyone's) before its first fragments are
-  // read; after that barrier every wave holds stage kt in registers, so
-  // stage kt+3 is copied into stage kt's slot. Three stages are issued ahead
-  // of the loop, so at the wait of iteration kt stages kt+1 and kt+2 are
-  // outstanding; stages past the end repeat the last tile and the final
-  // look-ahead reads are discarded.
+  // read; after that barrier every wave holds stage kt in registers, so the
+  // first half (H1) of stage kt+STAGES is copied into stage kt's slot during
+  // the second k32 step, and its second half (H2) during the first k32 step of
+  // the next iteration. At the wait of iteration kt the copies of stages
+  // kt+2 .. kt+STAGES-1 may still be outstanding. Stages past the end repeat
+  // the last tile and the final look-ahead reads are discarded.
   v4i fa0[4], fb0[2], fa1[4], fb1[2];
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NC + NC1) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NC + NC1) : "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   read_frags(0, 0, fa0, fb0);
@@ -296,14 +304,14 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
       read_frags(kt, ks + 1, fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
       if (ks == 0)
-        mfmas_dma(fa0, fb0, kt + 2, NC1, NC - NC1);  // H2 of stage kt+2
+        mfmas_dma(fa0, fb0, kt + STAGES - 1, NC1, NC - NC1);  // H2 of stage kt+STAGES-1
       else
         mfmas(fa0, fb0);
       __builtin_amdgcn_sched_barrier(0);
       if (ks + 2 < KS) {
         read_frags(kt, ks + 2, fa0, fb0);
       } else {
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(ACP + BCP) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NC) : "memory");
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
@@ -313,21 +321,15 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
       if (ks + 2 < KS)
         mfmas(fa1, fb1);
       else
-        mfmas_dma(fa1, fb1, kt + 3, 0, NC1);  // H1 of stage kt+3
+        mfmas_dma(fa1, fb1, kt + STAGES, 0, NC1);  // H1 of stage kt+STAGES
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated copies land before the ring is reused
 
   if (zp) {
-    // the WN waves of a row half publish 4 / WN subtiles each
-#pragma unroll
-    for (int ii = 0; ii < 4 / WN; ++ii) {
-      const int i = wn * (4 / WN) + ii;
-      const int32_t v = i == 0 ? xs[0] : i == 1 ? xs[1] : i == 2 ? xs[2] : xs[3];
-      const int32_t s = v + __shfl_xor(v, 32);
-      if (lane < 32) sXsum[wm * 128 + i * 32 + lane] = s;
-    }
+    const int32_t s = xs + __shfl_xor(xs, 32);
+    if (lane < 32) sXsum[wm * 128 + wn * 32 + lane] = s;
   }
   if (tid < BN) {
     const ColParams c = decode_col<EPI>(g, craw);
