@@ -644,6 +644,24 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                      timestamp_begin, max_initial_timestamp, logit_scale, as_stream(stream));
 }
 
+int iw_dtw(const float *x, int64_t rows, int64_t cols, int64_t ld, int8_t *trace, int64_t trace_ld,
+           iw_stream_t stream) {
+  IW_REQUIRE(rows > 0 && rows < 1024 && cols > 0 && cols < (1 << 30) && ld >= cols && trace_ld >= cols + 1,
+             "invalid DTW shape (1 <= rows < 1024)");
+  IW_REQUIRE(x && trace, "null tensor pointer");
+  return launch_dtw(x, rows, cols, ld, trace, trace_ld, as_stream(stream));
+}
+
+int iw_median_filter(const float *x, int64_t rows, int64_t cols, int64_t ld, int32_t width, float *y,
+                     int64_t y_ld, iw_stream_t stream) {
+  IW_REQUIRE(width > 0 && width % 2 == 1 && width <= 31, "filter width must be odd and at most 31");
+  IW_REQUIRE(rows >= 0 && cols > width / 2 && cols < (1 << 30) && ld >= cols && y_ld >= cols,
+             "invalid median filter shape (the row must be longer than width / 2)");
+  if (rows == 0) return IW_OK;
+  IW_REQUIRE(x && y, "null tensor pointer");
+  return launch_median_filter(x, rows, cols, ld, width, y, y_ld, as_stream(stream));
+}
+
 int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                    iw_stream_t stream) {
   IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 23) && ld >= cols,

@@ -55,6 +55,9 @@ int launch_greedy_step(const int8_t *logits, int64_t rows, int64_t cols, int64_t
                        int32_t *pos, int32_t pos_inc, hipStream_t s);
 int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, int64_t m,
                         int64_t t, hipStream_t s);
+int launch_dtw(const float *x, int64_t M, int64_t N, int64_t ld, int8_t *trace, int64_t tld, hipStream_t s);
+int launch_median_filter(const float *x, int64_t rows, int64_t cols, int64_t ld, int32_t width, float *y,
+                         int64_t ldy, hipStream_t s);
 int launch_greedy_step_filtered(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t *next,
                                 int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
                                 int32_t *pos, int32_t pos_inc, const uint32_t *mask, const uint32_t *mask_first,

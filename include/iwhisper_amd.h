@@ -320,6 +320,25 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                int32_t timestamp_begin, int32_t max_initial_timestamp,
                                float logit_scale, iw_stream_t stream);
 
+/* Dynamic time warping for word timestamps (triton_ops.py:13-40, dtw_cuda
+ * timing.py:108-141; it replaces the Triton kernel launch): over float32 costs
+ * x [rows][cols] (row stride ld; rows < 1024, the reference's M < BLOCK_SIZE),
+ * cost[i][j] = x[i-1][j-1] + min(cost[i-1][j-1], cost[i-1][j], cost[i][j-1])
+ * with cost[0][0] = 0 and +inf borders; writes trace [rows+1][cols+1] (row
+ * stride trace_ld >= cols + 1): trace[i][j] = 0, 1 or 2 for the first of the
+ * three predecessors holding the minimum (the reference kernel's store order),
+ * trace[0][*] = 2, trace[*][0] = 1, as timing.py's backtrace expects. */
+int iw_dtw(const float *x, int64_t rows, int64_t cols, int64_t ld, int8_t *trace, int64_t trace_ld,
+           iw_stream_t stream);
+
+/* Sliding median along the last dimension (median_filter, timing.py:19-55,
+ * replacing median_filter_cuda, triton_ops.py:43-109): y[r][t] = median of
+ * x[r][reflect(t - width/2 .. t + width/2)] (reflect padding without repeating
+ * the edge, F.pad(mode="reflect")). width odd, at most 31; cols > width / 2
+ * (the reference returns x unchanged otherwise). */
+int iw_median_filter(const float *x, int64_t rows, int64_t cols, int64_t ld, int32_t width, float *y,
+                     int64_t y_ld, iw_stream_t stream);
+
 /* Per-head gather into a [b][h][t][d] cache (the cross-attention K of
  * model_int.py:722-730, computed once per utterance):
  * dst[b*dst_sb + h*dst_sh + (t_offset+t)*dst_st + d] = src[b*src_sb + t*src_st + h*D + d]. */
