@@ -12,7 +12,7 @@ from .model_int import (  # noqa: F401
     set_attention_backend, set_conv1d_backend, set_decoder_backend, set_encoder_backend,
     set_gelu_backend, set_layernorm_backend, set_residual_backend)
 from .runtime import DecoderRunner, EncoderRunner, LogitFilters, greedy_decode  # noqa: F401
-from . import checkpoint  # noqa: F401
+from . import audio, checkpoint, timing  # noqa: F401
 from .checkpoint import (  # noqa: F401
     load_int_model, load_int_params, save_int_model, verify_int_model_roundtrip)
 

@@ -56,6 +56,7 @@ SIGNATURES = {
                                   _p],
     "iw_embed_tokens": [_p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _p],
     "iw_greedy_advance": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p],
+    "iw_log_mel": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64, _p, _p],
     "iw_dtw": [_p, _i64, _i64, _i64, _p, _i64, _p],
     "iw_median_filter": [_p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "iw_greedy_advance_filtered": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p, _p, _p,

@@ -644,6 +644,26 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                      timestamp_begin, max_initial_timestamp, logit_scale, as_stream(stream));
 }
 
+int iw_log_mel(const float *audio, int64_t batch, int64_t n_samples, int64_t audio_ld, const float *twiddle,
+               const float *window, const int32_t *filter_start, const int32_t *filter_len,
+               const int32_t *filter_offset, const float *filter_weights, int32_t n_taps, int32_t n_mels,
+               float *out, int64_t out_batch_stride, float *workspace, iw_stream_t stream) {
+  int max_mels = 0, max_taps = 0;
+  log_mel_limits(&max_mels, &max_taps);
+  IW_REQUIRE(batch >= 0 && n_samples > 256 && n_samples / 160 < (1 << 30) && audio_ld >= n_samples,
+             "invalid audio shape (more than 256 samples per row)");
+  IW_REQUIRE(n_mels > 0 && n_mels <= max_mels, "n_mels must be in 1 .. 128");
+  IW_REQUIRE(n_taps >= 0 && n_taps <= max_taps, "too many filterbank taps");
+  IW_REQUIRE(out_batch_stride >= (int64_t)n_mels * (n_samples / 160), "output batch stride too small");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(audio && twiddle && window && filter_start && filter_len && filter_offset && out && workspace &&
+                 (n_taps == 0 || filter_weights),
+             "null tensor pointer");
+  return launch_log_mel(audio, batch, n_samples, audio_ld, twiddle, window, filter_start, filter_len,
+                        filter_offset, filter_weights, n_taps, n_mels, out, out_batch_stride, workspace,
+                        as_stream(stream));
+}
+
 int iw_dtw(const float *x, int64_t rows, int64_t cols, int64_t ld, int8_t *trace, int64_t trace_ld,
            iw_stream_t stream) {
   IW_REQUIRE(rows > 0 && rows < 1024 && cols > 0 && cols < (1 << 30) && ld >= cols && trace_ld >= cols + 1,

@@ -320,6 +320,22 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                int32_t timestamp_begin, int32_t max_initial_timestamp,
                                float logit_scale, iw_stream_t stream);
 
+/* Log-mel spectrogram (log_mel_spectrogram, audio.py:216-267, with N_FFT =
+ * 512, HOP_LENGTH = 160): for each of `batch` rows of float32 audio
+ * (n_samples > 256, row stride audio_ld) and frame t < n_samples / 160, the
+ * 512-point FFT of the window-weighted frame centred at 160 t (reflect padding
+ * by 256), |X[k]|^2 for k = 0 .. 256, the mel projection
+ * mel[m] = sum_e w[off[m] + e] * |X[start[m] + e]|^2 (e < len[m]; the nonzero
+ * taps of the filterbank row m), then log10(max(mel, 1e-10)); finally per
+ * row y = max(y, max(row) - 8) / 4 + 1. out[b][m][t] (batch stride
+ * out_batch_stride >= n_mels * (n_samples / 160)). twiddle: 256 complex
+ * exp(-2 pi i j / 512) as (re, im) pairs; window: 512 Hann weights;
+ * n_mels <= 128, n_taps <= 2048; workspace: batch * ceil(frames / 64) floats. */
+int iw_log_mel(const float *audio, int64_t batch, int64_t n_samples, int64_t audio_ld, const float *twiddle,
+               const float *window, const int32_t *filter_start, const int32_t *filter_len,
+               const int32_t *filter_offset, const float *filter_weights, int32_t n_taps, int32_t n_mels,
+               float *out, int64_t out_batch_stride, float *workspace, iw_stream_t stream);
+
 /* Dynamic time warping for word timestamps (triton_ops.py:13-40, dtw_cuda
  * timing.py:108-141; it replaces the Triton kernel launch): over float32 costs
  * x [rows][cols] (row stride ld; rows < 1024, the reference's M < BLOCK_SIZE),
