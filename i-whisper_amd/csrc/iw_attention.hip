@@ -213,16 +213,23 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
     for (int kc = 0; kc < nkc; ++kc) {
       stage_k(kc);
       __syncthreads();
+      // a chunk of keys all below Tk and no mask: no per-key test
+      const bool full = !HAS_MASK && (kc + 1) * PF_KC <= a.Tk;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const v16i s = scores(sub);
         const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
+        if (full) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kbase0 + r;
-          bool ok = key < a.Tk;
-          if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
-          if (ok) mx = max(mx, s[r]);
+          for (int r = 0; r < 16; r += 2) mx = max(mx, max(s[r], s[r + 1]));
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kbase0 + r;
+            bool ok = key < a.Tk;
+            if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
+            if (ok) mx = max(mx, s[r]);
+          }
         }
       }
       __syncthreads();
@@ -232,6 +239,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
     const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
 
     // ---- pass 2: P = E(S - rmp1) and O = P . V ----
+    // requant constants (a shift >= 32 gives 0: multiplier 0 instead)
+    const int32_t qm24 = a.qk_s >= 32 ? 0 : (int32_t)a.qk_m;
+    const uint32_t qsh = a.qk_s >= 32 ? 0u : a.qk_s;
+    const uint32_t qhalf = qsh ? 1u << (qsh - 1) : 0u;
+    const uint32_t qw = min(qsh, 1u);
     v16i o[KS];
 #pragma unroll
     for (int t = 0; t < KS; ++t)
@@ -250,21 +262,38 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
         *reinterpret_cast<uint4 *>(&sVt[d * VLD + part * 16]) = val;
       }
       __syncthreads();
+      const bool full = !HAS_MASK && (kc + 1) * PF_KC <= a.Tk;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const v16i s = scores(sub);
         const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
-        uint32_t pw[4] = {0u, 0u, 0u, 0u};
+        // P of the 16 keys: requant (24-bit product: |score| < 2^21 and an
+        // 8-bit multiplier), round-half-away shift, int16 saturation, then
+        // the table at min((rowmax + 1 - h16) mod 2^16, size - 1)
+        // (keys past Tk or masked: P = 0, applied as a byte mask on the
+        // loaded value rather than a conditional write)
+        uint32_t pb[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kbase0 + r;
-          bool ok = key < a.Tk;
-          if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
-          const int32_t h16 = qk_requant16(s[r], a.qk_m, a.qk_s);
-          const uint32_t idx = min((uint32_t)(uint16_t)(rmp1 - (uint32_t)h16), (uint32_t)(IW_SEXP_LUT - 1));
-          const uint32_t pv = ok ? (uint32_t)sLut[idx] : 0u;
-          pw[r >> 2] |= pv << (8 * (r & 3));
+          uint32_t keep = 0xffu;
+          if (!full) {
+            const int key = kbase0 + r;
+            bool ok = key < a.Tk;
+            if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
+            keep = ok ? 0xffu : 0u;
+          }
+          const int32_t v = __mul24(s[r], qm24);
+          const uint32_t tr = (uint32_t)v + qhalf + (uint32_t)__builtin_amdgcn_sbfe(v, 31, qw);
+          const int32_t h16 = clampi((int32_t)tr >> qsh, -32768, 32767);
+          const uint32_t idx = min((rmp1 - (uint32_t)h16) & 0xffffu, (uint32_t)(IW_SEXP_LUT - 1));
+          pb[r] = (uint32_t)sLut[idx] & keep;
         }
+        uint32_t pw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          pw[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pb[4 * j + 3], pb[4 * j + 2], 0x0c0c0400u),
+                                        __builtin_amdgcn_perm(pb[4 * j + 1], pb[4 * j], 0x0c0c0400u),
+                                        0x05040100u);
         const uint32_t ones = 0x01010101u;
         psum = __builtin_amdgcn_udot4(pw[0], ones, psum, false);
         psum = __builtin_amdgcn_udot4(pw[1], ones, psum, false);
