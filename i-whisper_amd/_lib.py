@@ -61,7 +61,21 @@ SIGNATURES = {
     "iw_median_filter": [_p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "iw_greedy_advance_filtered": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p, _p, _p,
                                    _i32, _i32, _i32, _f, _p],
+    "iw_frag_pack": [_p, _i64, _i64, _i64, _p, _p],
+    "iw_linear8_frag": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _b, _b, _b, _p],
+    "iw_linear8_gelu_frag": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64,
+                             _i64, _b, _b, _b, _p],
+    "iw_linear32_residual15_frag": [_p, _p, _p, _p, _p, _p, _p, _u16, _p, _i64, _i64, _i64, _b, _b, _p],
+    "iw_linear8_qkv_cache_frag": [_p, _p, _p, _p, _p, _p, _i64, _i64, _b, _b, _p, _i64, _p, _i64, _i64,
+                                  _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "iw_layernorm32_frag": [_p, _p, _p, _u8, _i8, _u32, _i8, _u32, _p, _i64, _i64, _b, _p],
+    "iw_attention_decode_cache_frag": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
+                                       _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32, _p],
+    "iw_classifier_frag": [_p, _p, _u32, _i8, _p, _i64, _i64, _i64, _p],
 }
+
+# entry points that return a value rather than a status
+VALUE_FUNCS = {"iw_frag_bytes": ([_i64, _i64], C.c_int64)}
 
 _lock = threading.Lock()
 _lib = None
@@ -85,6 +99,10 @@ def load() -> C.CDLL:
                 fn = getattr(lib, name)
                 fn.argtypes = argtypes
                 fn.restype = C.c_int
+            for name, (argtypes, restype) in VALUE_FUNCS.items():
+                fn = getattr(lib, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
             lib.iw_last_error.restype = C.c_char_p
             lib.iw_last_error.argtypes = []
             lib.iw_abi_version.restype = C.c_int
@@ -101,5 +119,10 @@ def call(name: str, *args) -> None:
         raise IWError(msg)
 
 
+def value(name: str, *args):
+    """Call an entry point of VALUE_FUNCS and return its result."""
+    return getattr(load(), name)(*args)
+
+
 def exported_symbols() -> list[str]:
-    return ["iw_abi_version", "iw_last_error", *SIGNATURES.keys()]
+    return ["iw_abi_version", "iw_last_error", *SIGNATURES.keys(), *VALUE_FUNCS.keys()]

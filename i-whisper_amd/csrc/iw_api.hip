@@ -73,6 +73,128 @@ int check_gelu_counts(int64_t channels, int64_t luti_count, int64_t luto_count) 
   return IW_OK;
 }
 
+int qkv_cache_args(const int8_t *x, const int8_t *weight, const int32_t *bias, const int8_t *weight_zero,
+                   const uint32_t *multiplier, const int8_t *shift, int64_t M, int64_t K, bool has_bias,
+                   bool asymmetric, int8_t *q_out, int64_t q_ld, int8_t *k_cache, int64_t k_sb, int64_t k_sh,
+                   int64_t k_st, int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
+                   int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions, const int32_t *pos,
+                   GemmArgs *g, SkinnyScatter *sc) {
+  const int64_t N = 3 * channels;
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N, has_bias,
+                        asymmetric);
+  if (rc) return rc;
+  if (M == 0) return IW_OK;
+  IW_REQUIRE(M <= kSkinnyMaxRows, "the KV-cache QKV projection takes at most 128 rows");
+  IW_REQUIRE(channels > 0 && head_dim > 0 && channels % head_dim == 0, "invalid head geometry");
+  IW_REQUIRE(channels <= 0x3fffffff && tokens_per_row_group > 0 && M % tokens_per_row_group == 0,
+             "rows must be whole groups of tokens_per_row_group");
+  IW_REQUIRE(k_cache && v_cache && pos, "null cache pointer");
+  IW_REQUIRE(cache_positions > 0 && cache_positions <= 0x7fffffff && cache_positions <= v_sd,
+             "cache_positions must be positive and fit the transposed V rows");
+  *g = linear_args(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N, has_bias, asymmetric,
+                   EPI_L8);
+  sc->q = q_out;
+  sc->ldq = q_ld;
+  sc->k = k_cache;
+  sc->k_sb = k_sb;
+  sc->k_sh = k_sh;
+  sc->k_st = k_st;
+  sc->v = v_cache;
+  sc->v_sb = v_sb;
+  sc->v_sh = v_sh;
+  sc->v_sd = v_sd;
+  sc->C = (int)channels;
+  sc->D = (int)head_dim;
+  sc->T = (int)tokens_per_row_group;
+  sc->t_cap = (int)cache_positions;
+  sc->pos = pos;
+  return IW_OK;
+}
+
+int layernorm32_entry(const int16_t *x, const int8_t *weight, const int32_t *bias, uint8_t ln_multiplier,
+                      int8_t ln_shift, uint32_t out_multiplier, int8_t out_shift, uint32_t rsqrt_offset,
+                      int8_t *out, int64_t rows, int64_t hidden, bool has_bias, bool out_frag,
+                      iw_stream_t stream) {
+  IW_REQUIRE(layernorm_width_code(hidden) >= 0,
+             "unsupported LayerNorm hidden size: " + std::to_string(hidden));
+  IW_REQUIRE(rows >= 0, "invalid row count");
+  if (rows == 0) return IW_OK;
+  IW_REQUIRE(x && weight && out, "null tensor pointer");
+  IW_REQUIRE(!has_bias || bias, "has_bias set but bias is null");
+  IW_REQUIRE((reinterpret_cast<uintptr_t>(x) & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 3) == 0,
+             "LayerNorm input must be 8-byte and output 4-byte aligned");
+  return launch_layernorm32(x, weight, has_bias ? bias : nullptr, ln_multiplier, ln_shift,
+                            out_multiplier, out_shift, rsqrt_offset, out, rows, hidden,
+                            as_stream(stream), out_frag);
+}
+
+int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb, int64_t k_sh,
+                                 int64_t k_st, const int8_t *vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
+                                 int8_t *out, int64_t o_sb, int64_t batch, int64_t heads, int64_t head_dim,
+                                 int64_t k_length, const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
+                                 int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
+                                 uint32_t rsqrt_offset, bool out_frag, iw_stream_t stream) {
+  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
+  IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
+  IW_REQUIRE(head_dim == 64 || head_dim == 96 || head_dim == 128,
+             "decode attention supports head_dim 64, 96 and 128");
+  IW_REQUIRE(batch >= 0 && heads > 0 && k_length >= 0 && batch * heads <= 0x7fffffff,
+             "invalid attention shape");
+  // the key count on the device is k_length + *pos <= max_keys
+  IW_REQUIRE(max_keys >= k_length && max_keys <= kDecodeCacheMaxKeys && (pos || max_keys == k_length),
+             "at most 4096 keys, and max_keys bounds k_length + *pos");
+  IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((max_keys + 15) / 16) * 16,
+             "transposed V rows must be 16-byte multiples covering max_keys");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(q && k && vt && out, "null tensor pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(vt) | (uintptr_t)q_sb | (uintptr_t)k_sb |
+                          (uintptr_t)k_sh | (uintptr_t)k_st | (uintptr_t)v_sb | (uintptr_t)v_sh;
+  IW_REQUIRE((align & 15) == 0, "decode attention operands must be 16-byte aligned");
+  AttnArgs a;
+  a.q = q;
+  a.q_sb = q_sb;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_st = k_st;
+  a.vt = vt;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sd = v_sd;
+  a.vt_ld = v_sd;
+  a.out = out;
+  a.o_sb = o_sb;
+  a.B = (int32_t)batch;
+  a.H = (int32_t)heads;
+  a.Tq = 1;
+  a.Tk = (int32_t)k_length;
+  a.D = (int32_t)head_dim;
+  a.qk_m = qk_multiplier;
+  a.qk_s = (uint32_t)(qk_shift > 0 ? qk_shift : 0);
+  a.frac_bits = frac_bits;
+  a.av_m = av_multiplier;
+  a.av_s = (uint32_t)(av_shift < 0 ? 0 : (av_shift > 32 ? 32 : av_shift));
+  a.rsqrt_off = rsqrt_offset;
+  a.max_tk = (int32_t)max_keys;
+  if (out_frag) {
+    IW_REQUIRE(batch <= kSkinnyMaxRows && heads * head_dim <= kFragMaxK,
+               "a fragment-major attention output takes at most 128 rows of 5120 channels");
+    a.o_frag_kp = frag_kpad(heads * head_dim);
+  }
+  return launch_attn_decode_cache(a, pos, as_stream(stream));
+}
+
+// Fragment-major operands: sizes the kernels take and 16-byte alignment.
+int check_frag(const void *x, const void *w, int64_t M, int64_t K, int64_t N) {
+  IW_REQUIRE(M <= kSkinnyMaxRows, "the fragment-major GEMMs take at most 128 rows");
+  IW_REQUIRE(K <= kFragMaxK, "the fragment-major GEMMs take K <= 5120");
+  IW_REQUIRE(N <= 0x7fffff00LL, "N too large");
+  IW_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) == 0,
+             "fragment-major operands must be 16-byte aligned");
+  return IW_OK;
+}
+
 }  // namespace
 }  // namespace iw
 
@@ -178,17 +300,8 @@ int iw_layernorm32(const int16_t *x, const int8_t *weight, const int32_t *bias,
                    uint8_t ln_multiplier, int8_t ln_shift, uint32_t out_multiplier,
                    int8_t out_shift, uint32_t rsqrt_offset, int8_t *out, int64_t rows,
                    int64_t hidden, bool has_bias, iw_stream_t stream) {
-  IW_REQUIRE(layernorm_width_code(hidden) >= 0,
-             "unsupported LayerNorm hidden size: " + std::to_string(hidden));
-  IW_REQUIRE(rows >= 0, "invalid row count");
-  if (rows == 0) return IW_OK;
-  IW_REQUIRE(x && weight && out, "null tensor pointer");
-  IW_REQUIRE(!has_bias || bias, "has_bias set but bias is null");
-  IW_REQUIRE((reinterpret_cast<uintptr_t>(x) & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 3) == 0,
-             "LayerNorm input must be 8-byte and output 4-byte aligned");
-  return launch_layernorm32(x, weight, has_bias ? bias : nullptr, ln_multiplier, ln_shift,
-                            out_multiplier, out_shift, rsqrt_offset, out, rows, hidden,
-                            as_stream(stream));
+  return layernorm32_entry(x, weight, bias, ln_multiplier, ln_shift, out_multiplier, out_shift, rsqrt_offset, out,
+                           rows, hidden, has_bias, false, stream);
 }
 
 int iw_layernorm32_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t offset,
@@ -516,37 +629,13 @@ int iw_linear8_qkv_cache(const int8_t *x, const int8_t *weight, const int32_t *b
                          int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
                          int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
                          const int32_t *pos, iw_stream_t stream) {
-  const int64_t N = 3 * channels;
-  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N, has_bias,
-                        asymmetric);
-  if (rc) return rc;
-  if (M == 0) return IW_OK;
-  IW_REQUIRE(M <= kSkinnyMaxRows, "the KV-cache QKV projection takes at most 128 rows");
-  IW_REQUIRE(channels > 0 && head_dim > 0 && channels % head_dim == 0, "invalid head geometry");
-  IW_REQUIRE(channels <= 0x3fffffff && tokens_per_row_group > 0 && M % tokens_per_row_group == 0,
-             "rows must be whole groups of tokens_per_row_group");
-  IW_REQUIRE(k_cache && v_cache && pos, "null cache pointer");
-  IW_REQUIRE(cache_positions > 0 && cache_positions <= 0x7fffffff && cache_positions <= v_sd,
-             "cache_positions must be positive and fit the transposed V rows");
-  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N,
-                           has_bias, asymmetric, EPI_L8);
-  IW_REQUIRE(gemm_skinny_eligible(g), "QKV projection needs K % 16 == 0 and 16-byte aligned operands");
+  GemmArgs g;
   SkinnyScatter sc;
-  sc.q = q_out;
-  sc.ldq = q_ld;
-  sc.k = k_cache;
-  sc.k_sb = k_sb;
-  sc.k_sh = k_sh;
-  sc.k_st = k_st;
-  sc.v = v_cache;
-  sc.v_sb = v_sb;
-  sc.v_sh = v_sh;
-  sc.v_sd = v_sd;
-  sc.C = (int)channels;
-  sc.D = (int)head_dim;
-  sc.T = (int)tokens_per_row_group;
-  sc.t_cap = (int)cache_positions;
-  sc.pos = pos;
+  int rc = qkv_cache_args(x, weight, bias, weight_zero, multiplier, shift, M, K, has_bias, asymmetric, q_out,
+                          q_ld, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_sd, channels, head_dim,
+                          tokens_per_row_group, cache_positions, pos, &g, &sc);
+  if (rc || M == 0) return rc;
+  IW_REQUIRE(gemm_skinny_eligible(g), "QKV projection needs K % 16 == 0 and 16-byte aligned operands");
   return gemm_skinny(g, &sc, as_stream(stream));
 }
 
@@ -557,50 +646,9 @@ int iw_attention_decode_cache(const int8_t *q, int64_t q_sb, const int8_t *k, in
                               const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                               int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
                               int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream) {
-  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
-  IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
-  IW_REQUIRE(head_dim == 64 || head_dim == 96 || head_dim == 128,
-             "decode attention supports head_dim 64, 96 and 128");
-  IW_REQUIRE(batch >= 0 && heads > 0 && k_length >= 0 && batch * heads <= 0x7fffffff,
-             "invalid attention shape");
-  // the key count on the device is k_length + *pos <= max_keys
-  IW_REQUIRE(max_keys >= k_length && max_keys <= kDecodeCacheMaxKeys && (pos || max_keys == k_length),
-             "at most 4096 keys, and max_keys bounds k_length + *pos");
-  IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((max_keys + 15) / 16) * 16,
-             "transposed V rows must be 16-byte multiples covering max_keys");
-  if (batch == 0) return IW_OK;
-  IW_REQUIRE(q && k && vt && out, "null tensor pointer");
-  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
-                          reinterpret_cast<uintptr_t>(vt) | (uintptr_t)q_sb | (uintptr_t)k_sb |
-                          (uintptr_t)k_sh | (uintptr_t)k_st | (uintptr_t)v_sb | (uintptr_t)v_sh;
-  IW_REQUIRE((align & 15) == 0, "decode attention operands must be 16-byte aligned");
-  AttnArgs a;
-  a.q = q;
-  a.q_sb = q_sb;
-  a.k = k;
-  a.k_sb = k_sb;
-  a.k_sh = k_sh;
-  a.k_st = k_st;
-  a.vt = vt;
-  a.v_sb = v_sb;
-  a.v_sh = v_sh;
-  a.v_sd = v_sd;
-  a.vt_ld = v_sd;
-  a.out = out;
-  a.o_sb = o_sb;
-  a.B = (int32_t)batch;
-  a.H = (int32_t)heads;
-  a.Tq = 1;
-  a.Tk = (int32_t)k_length;
-  a.D = (int32_t)head_dim;
-  a.qk_m = qk_multiplier;
-  a.qk_s = (uint32_t)(qk_shift > 0 ? qk_shift : 0);
-  a.frac_bits = frac_bits;
-  a.av_m = av_multiplier;
-  a.av_s = (uint32_t)(av_shift < 0 ? 0 : (av_shift > 32 ? 32 : av_shift));
-  a.rsqrt_off = rsqrt_offset;
-  a.max_tk = (int32_t)max_keys;
-  return launch_attn_decode_cache(a, pos, as_stream(stream));
+  return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, out, o_sb, batch, heads,
+                                      head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
+                                      av_multiplier, av_shift, rsqrt_offset, false, stream);
 }
 
 int iw_embed_tokens(const int64_t *tokens, const int8_t *table, const int8_t *pe,
@@ -689,6 +737,140 @@ int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int6
   if (rows == 0) return IW_OK;
   IW_REQUIRE(x && out, "null tensor pointer");
   return launch_argmax_rows(x, rows, cols, ld, out, as_stream(stream));
+}
+
+// ---- fragment-major decode operands ----
+
+int64_t iw_frag_bytes(int64_t rows, int64_t cols) {
+  if (rows < 0 || cols < 0 || cols > kFragMaxK) return 0;
+  return frag_rpad(rows) * frag_kpad(cols);
+}
+
+int iw_frag_pack(const int8_t *src, int64_t rows, int64_t cols, int64_t ld, int8_t *dst, iw_stream_t stream) {
+  IW_REQUIRE(rows >= 0 && cols >= 0 && cols <= kFragMaxK, "fragment-major matrices have at most 5120 columns");
+  IW_REQUIRE(ld >= cols, "ld must be at least cols");
+  if (rows == 0 || cols == 0) return IW_OK;
+  IW_REQUIRE(src && dst, "null tensor pointer");
+  IW_REQUIRE((reinterpret_cast<uintptr_t>(dst) & 15) == 0, "dst must be 16-byte aligned");
+  return launch_frag_pack(src, rows, cols, ld, dst, as_stream(stream));
+}
+
+int iw_linear8_frag(const int8_t *x, const int8_t *weight, const int32_t *bias, const int8_t *weight_zero,
+                    const uint32_t *multiplier, const int8_t *shift, int8_t *out, int64_t M, int64_t K, int64_t N,
+                    bool has_bias, bool asymmetric, bool out_frag, iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric);
+  if (rc || M == 0) return rc;
+  rc = check_frag(x, weight, M, K, N);
+  if (rc) return rc;
+  IW_REQUIRE(!out_frag || N <= kFragMaxK, "a fragment-major output has at most 5120 columns");
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric,
+                           EPI_L8);
+  if (out_frag) g.ldc = frag_kpad(N);
+  return gemm_frag(g, nullptr, out_frag, as_stream(stream));
+}
+
+int iw_linear8_gelu_frag(const int8_t *x, const int8_t *weight, const int32_t *bias, const int8_t *weight_zero,
+                         const uint32_t *multiplier, const int8_t *shift, const uint8_t *lut,
+                         const uint8_t *luti_multiplier, const int8_t *luti_shift, const uint8_t *luto_multiplier,
+                         const int8_t *luto_shift, int64_t luti_count, int64_t luto_count, int8_t *out, int64_t M,
+                         int64_t K, int64_t N, bool has_bias, bool asymmetric, bool out_frag,
+                         iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric);
+  if (rc) return rc;
+  rc = check_gelu_counts(N, luti_count, luto_count);
+  if (rc || M == 0) return rc;
+  rc = check_frag(x, weight, M, K, N);
+  if (rc) return rc;
+  IW_REQUIRE(!out_frag || N <= kFragMaxK, "a fragment-major output has at most 5120 columns");
+  IW_REQUIRE(lut && luti_multiplier && luti_shift && luto_multiplier && luto_shift, "null GeLU parameter pointer");
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric,
+                           EPI_L8);
+  g.lut = lut;
+  g.luti_m = luti_multiplier;
+  g.luti_s = luti_shift;
+  g.luto_m = luto_multiplier;
+  g.luto_s = luto_shift;
+  g.luti_pc = luti_count != 1;
+  g.luto_pc = luto_count != 1;
+  if (out_frag) g.ldc = frag_kpad(N);
+  return gemm_frag(g, nullptr, out_frag, as_stream(stream));
+}
+
+int iw_linear32_residual15_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                                const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                                const int16_t *residual, uint16_t residual_multiplier, int16_t *out, int64_t M,
+                                int64_t K, int64_t N, bool has_bias, bool asymmetric, iw_stream_t stream) {
+  int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric);
+  if (rc || M == 0) return rc;
+  rc = check_frag(x, weight, M, K, N);
+  if (rc) return rc;
+  IW_REQUIRE(residual, "null residual pointer");
+  GemmArgs g = linear_args(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric,
+                           EPI_L32RES);
+  g.res = residual;
+  g.ldres = N;
+  g.res_mult = residual_multiplier;
+  return gemm_frag(g, nullptr, false, as_stream(stream));
+}
+
+int iw_linear8_qkv_cache_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                              const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                              int64_t M, int64_t K, bool has_bias, bool asymmetric, int8_t *q_out, int64_t q_ld,
+                              int8_t *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st, int8_t *v_cache,
+                              int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels, int64_t head_dim,
+                              int64_t tokens_per_row_group, int64_t cache_positions, const int32_t *pos,
+                              iw_stream_t stream) {
+  GemmArgs g;
+  SkinnyScatter sc;
+  int rc = qkv_cache_args(x, weight, bias, weight_zero, multiplier, shift, M, K, has_bias, asymmetric, q_out,
+                          q_ld, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_sd, channels, head_dim,
+                          tokens_per_row_group, cache_positions, pos, &g, &sc);
+  if (rc || M == 0) return rc;
+  rc = check_frag(x, weight, M, K, 3 * channels);
+  if (rc) return rc;
+  return gemm_frag(g, &sc, false, as_stream(stream));
+}
+
+int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *bias, uint8_t ln_multiplier,
+                        int8_t ln_shift, uint32_t out_multiplier, int8_t out_shift, uint32_t rsqrt_offset,
+                        int8_t *out, int64_t rows, int64_t hidden, bool has_bias, iw_stream_t stream) {
+  return layernorm32_entry(x, weight, bias, ln_multiplier, ln_shift, out_multiplier, out_shift, rsqrt_offset, out,
+                           rows, hidden, has_bias, true, stream);
+}
+
+int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb, int64_t k_sh,
+                                   int64_t k_st, const int8_t *vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
+                                   int8_t *out, int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
+                                   const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier, int8_t qk_shift,
+                                   int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
+                                   uint32_t rsqrt_offset, iw_stream_t stream) {
+  return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, out, 0, batch, heads,
+                                      head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
+                                      av_multiplier, av_shift, rsqrt_offset, true, stream);
+}
+
+int iw_classifier_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift, int8_t *out,
+                       int64_t M, int64_t K, int64_t N, iw_stream_t stream) {
+  IW_REQUIRE(K > 0, "hidden size must be positive");
+  IW_REQUIRE(N > 0, "vocabulary size must be positive");
+  IW_REQUIRE(M >= 0, "invalid row count");
+  if (M == 0) return IW_OK;
+  IW_REQUIRE(x && weight && out, "null tensor pointer");
+  int rc = check_frag(x, weight, M, K, N);
+  if (rc) return rc;
+  GemmArgs g;
+  g.a = x;
+  g.b = weight;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.epi = EPI_S8;
+  g.mult_pc = 0;
+  g.out = out;
+  g.ldc = N;
+  g.scalar_mult = multiplier;
+  g.scalar_shift = shift;
+  return gemm_frag(g, nullptr, false, as_stream(stream));
 }
 
 }  // extern "C"

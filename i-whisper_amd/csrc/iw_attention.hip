@@ -16,11 +16,19 @@
 //   attn_decode   - streaming kernel for a few query rows over a KV cache
 //                   (decoder self- and cross-attention).
 #include "iw_common.hpp"
+#include "iw_gemm.hpp"
 #include "iw_kernels.hpp"
 
 namespace iw {
 
 namespace {
+
+// Output element (b, c) of the decode kernels over the caches: row-major at
+// b * o_sb + c, or the fragment-major image of [B][H*D] feeding the
+// out-projection GEMM.
+__device__ __forceinline__ int64_t decode_out_index(const AttnArgs &a, int64_t b, int c) {
+  return a.o_frag_kp ? frag_offset(b, c, a.o_frag_kp) : b * a.o_sb + c;
+}
 
 __device__ __forceinline__ int32_t qk_requant16(int32_t acc, uint32_t m, uint32_t s) {
   // (int32)(acc * m) modulo 2^32, Rshift, saturate to int16
@@ -637,7 +645,7 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
     int32_t y = rshift((int32_t)(accv * (uint32_t)inv), a.rsqrt_off);
     y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
     y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
-    a.out[b * a.o_sb + (int64_t)h * D + d] = (int8_t)clampi(y, -127, 127);
+    a.out[decode_out_index(a, b, h * D + d)] = (int8_t)clampi(y, -127, 127);
   }
 }
 
@@ -859,7 +867,7 @@ __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, con
       int32_t y = rshift((int32_t)(v * (uint32_t)inv), a.rsqrt_off);
       y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
       y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
-      a.out[b * a.o_sb + (int64_t)h * D + vrow + u * RPD] = (int8_t)clampi(y, -127, 127);
+      a.out[decode_out_index(a, b, h * D + vrow + u * RPD)] = (int8_t)clampi(y, -127, 127);
     }
   }
 }

@@ -80,6 +80,26 @@ constexpr int64_t kSkinnyMaxRows = 128;
 bool gemm_skinny_eligible(const GemmArgs &g);
 int gemm_skinny(const GemmArgs &g, const SkinnyScatter *scatter, hipStream_t s);
 
+// Fragment-major operands of the one-token decode GEMMs (iw_gemm_frag.hip).
+// An int8 matrix X[R][K] is stored as [R/32][Kp/32][64][16]: block (i, s)
+// is the 1 KB register image of the v_mfma_i32_32x32x32_i8 operand for rows
+// 32i .. 32i+31 and k = 32s .. 32s+31, lane l holding row 32i + l % 32,
+// bytes k = 32s + 16 (l / 32) .. +15. R is padded to a multiple of 32 and K
+// to Kp = a multiple of 320 (frag_kpad); the padding holds zeros, which add
+// nothing to a product or a row sum.
+constexpr int64_t kFragMaxK = 5120;
+
+__host__ __device__ inline int64_t frag_kpad(int64_t k) { return (k + 319) / 320 * 320; }
+__host__ __device__ inline int64_t frag_rpad(int64_t r) { return (r + 31) / 32 * 32; }
+__host__ __device__ inline int64_t frag_offset(int64_t r, int64_t k, int64_t kp) {
+  return (r >> 5) * 32 * kp + (k >> 5) * 1024 + ((r & 31) + ((k >> 4) & 1) * 32) * 16 + (k & 15);
+}
+
+// a and b fragment-major with padded K = frag_kpad(K); out_frag: the int8
+// output is itself written fragment-major (padded K = frag_kpad(N)).
+int gemm_frag(const GemmArgs &g, const SkinnyScatter *scatter, bool out_frag, hipStream_t s);
+int launch_frag_pack(const int8_t *src, int64_t rows, int64_t cols, int64_t ld, int8_t *dst, hipStream_t s);
+
 // Rows from which the 256 x 128 tile kernel (iw_gemm_big.hip) is used.
 constexpr int64_t kBigGemmMinRows = 8192;
 

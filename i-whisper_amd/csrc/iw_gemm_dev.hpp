@@ -240,5 +240,57 @@ __device__ __forceinline__ uint32_t corrected_k32k(int32_t acc, int32_t xsum, co
   return (uint32_t)acc - (uint32_t)__mul24((int32_t)c.wz, xsum) + c.bias;
 }
 
+// Epilogue of one output element of the decode GEMMs: `a` is the
+// accumulator after the zero-point and bias terms, m / n its row and column,
+// `res` the residual input of Linear32 + residual15.
+template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG = false>
+__device__ __forceinline__ void skinny_store(const GemmArgs &g, const SkinnyScatter &sc,
+                                             const ColParams &c, const uint8_t *lut, int pos, int m,
+                                             int n, uint32_t a, int32_t res) {
+  if (EPI == EPI_L8 || EPI == EPI_S8) {
+    int32_t y = clampi(apply_shift(mulh_su((int32_t)a, c.mult), c.shift), -127, 127);
+    if (GELU) y = gelu_dec(y, lut, c);
+    if (SCATTER) {
+      // columns [0, C): Q; [C, 2C): K appended at position pos + (m % T)
+      // of the [B, H, T_cache, D] cache; [2C, 3C): V appended to the
+      // transposed [B, H, D, T_cache] cache
+      const int b = m / sc.T, t = pos + m % sc.T;
+      if (n < sc.C) {
+        sc.q[(int64_t)m * sc.ldq + n] = (int8_t)y;
+      } else if (t < 0 || t >= sc.t_cap) {
+        // position outside the cache: nothing is appended
+      } else if (n < 2 * sc.C) {
+        const int h = (n - sc.C) / sc.D, d = (n - sc.C) % sc.D;
+        sc.k[(int64_t)b * sc.k_sb + (int64_t)h * sc.k_sh + (int64_t)t * sc.k_st + d] = (int8_t)y;
+      } else {
+        const int h = (n - 2 * sc.C) / sc.D, d = (n - 2 * sc.C) % sc.D;
+        sc.v[(int64_t)b * sc.v_sb + (int64_t)h * sc.v_sh + (int64_t)d * sc.v_sd + t] = (int8_t)y;
+      }
+    } else if (OUT_FRAG) {
+      // fragment-major output: g.ldc is its padded K
+      reinterpret_cast<int8_t *>(g.out)[frag_offset(m, n, g.ldc)] = (int8_t)y;
+    } else {
+      reinterpret_cast<int8_t *>(g.out)[(int64_t)m * g.ldc + n] = (int8_t)y;
+    }
+  } else {
+    const int32_t br = (int32_t)((uint32_t)mulh_su((int32_t)a, c.mult) << c.shift.sh);
+    if (EPI == EPI_L32) {
+      reinterpret_cast<int32_t *>(g.out)[(int64_t)m * g.ldc + n] = br;
+    } else {
+      const uint32_t v = (uint32_t)br + (uint32_t)(res * (int32_t)g.res_mult);
+      const int32_t y = clampi(rshift_pos((int32_t)v, 15), -16383, 16383);
+      reinterpret_cast<int16_t *>(g.out)[(int64_t)m * g.ldc + n] = (int16_t)y;
+    }
+  }
+}
+
+__device__ __forceinline__ int32_t sum16v(v4i v, int32_t acc) {
+  const int ones = 0x01010101;
+  acc = __builtin_amdgcn_sdot4(v[0], ones, acc, false);
+  acc = __builtin_amdgcn_sdot4(v[1], ones, acc, false);
+  acc = __builtin_amdgcn_sdot4(v[2], ones, acc, false);
+  return __builtin_amdgcn_sdot4(v[3], ones, acc, false);
+}
+
 }  // namespace gemm
 }  // namespace iw

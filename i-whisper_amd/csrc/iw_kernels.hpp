@@ -32,12 +32,14 @@ struct AttnArgs {
   uint32_t rsqrt_off = 16;
   const uint8_t *lut = nullptr;  // IW_SEXP_LUT entries for frac_bits
   int32_t max_tk = 0;            // decode over caches: bound of Tk + *pos
+  int64_t o_frag_kp = 0;         // decode over caches: > 0 writes out fragment-major [B][H*D]
 };
 
 int layernorm_width_code(int64_t h);
+// out_frag: out is the fragment-major image of [rows][hidden] (rows <= 128)
 int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
                        int8_t ln_s, uint32_t out_m, int8_t out_s, uint32_t rsqrt_off, int8_t *out,
-                       int64_t rows, int64_t hidden, hipStream_t s);
+                       int64_t rows, int64_t hidden, hipStream_t s, bool out_frag = false);
 int launch_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t off, hipStream_t s);
 int launch_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_m, const int8_t *luti_s,
                 const uint8_t *luto_m, const int8_t *luto_s, int8_t *out, int64_t numel,

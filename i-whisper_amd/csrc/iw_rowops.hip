@@ -3,6 +3,7 @@
 // the greedy argmax. All are HBM-bound; each reads and writes its operands
 // once.
 #include "iw_common.hpp"
+#include "iw_gemm.hpp"
 #include "iw_kernels.hpp"
 
 namespace iw {
@@ -171,7 +172,8 @@ constexpr int LNR_MAX = 5;  // 1280 / 256
 __global__ __launch_bounds__(256) void layernorm32_row_kernel(
     const int16_t *__restrict__ x, const int8_t *__restrict__ gamma,
     const int32_t *__restrict__ beta, uint32_t ln_m, int32_t ln_s, uint32_t out_m,
-    int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int hidden, int code) {
+    int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int hidden, int code,
+    int64_t out_frag_kp) {
   __shared__ uint32_t sA[4], sB[4], sC[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
@@ -229,7 +231,12 @@ __global__ __launch_bounds__(256) void layernorm32_row_kernel(
       const uint32_t t = (uint32_t)d * (uint32_t)inv * ln_m;
       const int32_t y = clampi(rshift((int32_t)t, nshift), -16383, 16383);
       const uint32_t a = (uint32_t)y * (uint32_t)gm[j] + (uint32_t)bt[j];
-      orow[e] = (int8_t)clampi(rshift(mulh((int32_t)a, out_m), (uint32_t)out_s), -127, 127);
+      const int8_t yo = (int8_t)clampi(rshift(mulh((int32_t)a, out_m), (uint32_t)out_s), -127, 127);
+      // row-major, or the fragment-major operand image of a decode GEMM
+      if (out_frag_kp)
+        out[frag_offset(row, e, out_frag_kp)] = yo;
+      else
+        orow[e] = yo;
     }
   }
 }
@@ -607,15 +614,16 @@ int layernorm_width_code(int64_t h) {
 
 int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
                        int8_t ln_s, uint32_t out_m, int8_t out_s, uint32_t rsqrt_off, int8_t *out,
-                       int64_t rows, int64_t hidden, hipStream_t s) {
+                       int64_t rows, int64_t hidden, hipStream_t s, bool out_frag) {
   const int code = layernorm_width_code(hidden);
   if (code < 0) return fail("unsupported LayerNorm hidden size: " + std::to_string(hidden));
   if (rows == 0) return 0;
+  if (out_frag && rows > kSkinnyMaxRows) return fail("a fragment-major LayerNorm output takes at most 128 rows");
   if (rows <= kLnRowBlockMaxRows) {
     // few rows (a decode step): a block of 256 threads per row
     hipLaunchKernelGGL(layernorm32_row_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, gamma, beta,
                        (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, (int)hidden,
-                       code);
+                       code, out_frag ? frag_kpad(hidden) : (int64_t)0);
     return check_launch("layernorm32_row_kernel");
   }
   // one row per wave, four rows per block

@@ -94,6 +94,56 @@ def _mlp_gelu(block: ResidualAttentionBlock_int, x_ptr: int, M: int, out: torch.
     return out
 
 
+def _frag_pack(w: torch.Tensor) -> torch.Tensor:
+    """Fragment-major image of a row-major int8 [R, K] matrix (zero padded)."""
+    R, K = w.shape
+    out = torch.zeros(_lib.value("iw_frag_bytes", R, K), dtype=torch.int8, device=w.device)
+    _lib.call("iw_frag_pack", w.data_ptr(), R, K, w.stride(0), out.data_ptr(), _stream())
+    return out
+
+
+def _frag_buffer(rows: int, cols: int, dev) -> torch.Tensor:
+    """A zeroed fragment-major [rows, cols] activation buffer: producers write
+    only the real rows and columns, so the padding stays zero."""
+    return torch.zeros(_lib.value("iw_frag_bytes", rows, cols), dtype=torch.int8, device=dev)
+
+
+def _ln_frag(ln, x: torch.Tensor, rows: int, out: torch.Tensor):
+    s = ln._scalars()
+    _lib.call("iw_layernorm32_frag", x.data_ptr(), ln.weight.data_ptr(), _ptr(ln.bias), s["lm"],
+              s["ls"], s["om"], s["os"], ln.offset, out.data_ptr(), rows, ln.normalized_shape[0],
+              ln.bias is not None, _stream())
+    return out
+
+
+class _FragLinear:
+    """A LinearBase layer (or a _FusedLinear) with its weight packed
+    fragment-major for the one-token decode GEMMs."""
+
+    def __init__(self, layer):
+        fused = isinstance(layer, _FusedLinear)
+        self.K = layer.K if fused else layer.in_features
+        self.N = layer.N if fused else layer.out_features
+        self.w = _frag_pack(layer.weight)
+        self.bias = layer.bias
+        self.wz = layer.wz if fused else (layer.wgt_zeros if layer.asym else None)
+        self.mult = layer.mult if fused else layer.req_multiplier
+        self.shift = layer.shift if fused else layer.req_shiftmount
+
+    def args(self):
+        return (self.w.data_ptr(), _ptr(self.bias), _ptr(self.wz), self.mult.data_ptr(),
+                self.shift.data_ptr())
+
+    def linear8(self, xf: torch.Tensor, M: int, out: torch.Tensor, out_frag: bool = False):
+        _lib.call("iw_linear8_frag", xf.data_ptr(), *self.args(), out.data_ptr(), M, self.K, self.N,
+                  self.bias is not None, self.wz is not None, out_frag, _stream())
+
+    def linear32_res(self, xf: torch.Tensor, M: int, res: torch.Tensor, res_mult: int):
+        _lib.call("iw_linear32_residual15_frag", xf.data_ptr(), *self.args(), res.data_ptr(), res_mult,
+                  res.data_ptr(), M, self.K, self.N, self.bias is not None, self.wz is not None,
+                  _stream())
+
+
 class EncoderRunner:
     """AudioEncoder_int forward for a fixed batch with preallocated activations."""
 
@@ -213,7 +263,7 @@ class DecoderRunner:
 
     def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int,
                  max_steps: Optional[int] = None, use_graph: bool = True,
-                 filters: Optional[LogitFilters] = None):
+                 filters: Optional[LogitFilters] = None, frag: bool = True):
         self.dec = decoder
         self.B = batch
         C, H = decoder.n_state, decoder.n_head
@@ -242,6 +292,19 @@ class DecoderRunner:
         self.wv = torch.empty((batch, C), **i8)
         self.f8 = torch.empty((batch, 4 * C), **i8)
         self.logits = torch.empty((batch, decoder.n_vocab), **i8)
+        # fragment-major weights and activations of the one-token step
+        self.frag = frag and batch <= 128 and 4 * C <= 5120
+        if self.frag:
+            self.f_qkv = [_FragLinear(f) for f in self.self_qkv]
+            self.f_out = [_FragLinear(b.attn.out) for b in decoder.blocks]
+            self.f_cq = [_FragLinear(b.cross_attn.query) for b in decoder.blocks]
+            self.f_co = [_FragLinear(b.cross_attn.out) for b in decoder.blocks]
+            self.f_fc1 = [_FragLinear(b.mlp[0]) for b in decoder.blocks]
+            self.f_fc2 = [_FragLinear(b.mlp[2]) for b in decoder.blocks]
+            self.f_emb = _frag_pack(decoder.token_embedding.weight)
+            self.h8f = _frag_buffer(batch, C, dev)
+            self.wvf = _frag_buffer(batch, C, dev)
+            self.f8f = _frag_buffer(batch, 4 * C, dev)
         # device-side decode state
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)   # tokens in the self caches
         self.step_no = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -311,9 +374,15 @@ class DecoderRunner:
         """Final LayerNorm of the last position, classifier, argmax, record, advance."""
         dec = self.dec
         sc = dec.scalars()
-        _ln(dec.ln, x_last, self.B, self.h8)
-        _lib.call("iw_classifier", self.h8.data_ptr(), dec.token_embedding.weight.data_ptr(), sc["cm"],
-                  sc["cs"], self.logits.data_ptr(), self.B, self.C, dec.n_vocab, _stream())
+        if self.frag:
+            _ln_frag(dec.ln, x_last, self.B, self.h8f)
+            _lib.call("iw_classifier_frag", self.h8f.data_ptr(), self.f_emb.data_ptr(), sc["cm"], sc["cs"],
+                      self.logits.data_ptr(), self.B, self.C, dec.n_vocab, _stream())
+        else:
+            _ln(dec.ln, x_last, self.B, self.h8)
+            _lib.call("iw_classifier", self.h8.data_ptr(), dec.token_embedding.weight.data_ptr(),
+                      sc["cm"], sc["cs"], self.logits.data_ptr(), self.B, self.C, dec.n_vocab,
+                      _stream())
         f = self.filters
         if f is None:
             _lib.call("iw_greedy_advance", self.logits.data_ptr(), self.B, dec.n_vocab, dec.n_vocab,
@@ -376,6 +445,10 @@ class DecoderRunner:
         _lib.call("iw_embed_tokens", self.tokens.data_ptr(), dec.token_embedding.weight.data_ptr(),
                   dec.positional_embedding.data_ptr(), dec.n_ctx, self.pos.data_ptr(),
                   sc0["m16"].data_ptr(), sc0["s"].data_ptr(), self.x16.data_ptr(), B, C, _stream())
+        if self.frag:
+            self._decode_layers_frag()
+            self._finish(self.x16, 1)
+            return
         x16, h8, q8, wv, f8 = self.x16, self.h8, self.q8, self.wv, self.f8
         for l, blk in enumerate(dec.blocks):
             sc = blk._scalars()
@@ -401,6 +474,45 @@ class DecoderRunner:
             _mlp_gelu(blk, h8.data_ptr(), B, f8)
             _lin32_res(blk.mlp[2], f8.data_ptr(), B, x16, sc["m"])
         self._finish(x16, 1)
+
+    def _decode_layers_frag(self):
+        """The decoder blocks of one token step on fragment-major operands: each
+        LayerNorm, attention and FC1 writes the operand image its GEMM reads."""
+        dec = self.dec
+        B, C, H, D = self.B, self.C, self.H, self.D
+        x16, q8, h8f, wvf, f8f = self.x16, self.q8, self.h8f, self.wvf, self.f8f
+        for l, blk in enumerate(dec.blocks):
+            sc = blk._scalars()
+            fq = self.f_qkv[l]
+            _ln_frag(blk.attn_ln, x16, B, h8f)
+            _lib.call("iw_linear8_qkv_cache_frag", h8f.data_ptr(), *fq.args(), B, C, True, True,
+                      q8.data_ptr(), C, self.k_self[l].data_ptr(), H * self.Tcap * D, self.Tcap * D, D,
+                      self.vt_self[l].data_ptr(), H * D * self.tcap16, D * self.tcap16, self.tcap16, C,
+                      D, 1, self.Tcap, self.pos.data_ptr(), _stream())
+            s = blk.attn._scalars()
+            _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_self[l].data_ptr(),
+                      H * self.Tcap * D, self.Tcap * D, D, self.vt_self[l].data_ptr(),
+                      H * D * self.tcap16, D * self.tcap16, self.tcap16, wvf.data_ptr(), B, H, D, 1,
+                      self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
+                      blk.attn.rsqrt_offset, _stream())
+            self.f_out[l].linear32_res(wvf, B, x16, sc["a"])
+            _ln_frag(blk.cross_attn_ln, x16, B, h8f)
+            self.f_cq[l].linear8(h8f, B, q8)
+            s = blk.cross_attn._scalars()
+            Ta = self.Ta
+            _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_cross[l].data_ptr(),
+                      H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
+                      D * self.ta16, self.ta16, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
+                      s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
+            self.f_co[l].linear32_res(wvf, B, x16, sc["c"])
+            _ln_frag(blk.mlp_ln, x16, B, h8f)
+            fc1, gelu = blk.mlp[0], blk.mlp[1]
+            lut, im, is_, om, os_, ci, co = gelu.gelu_ptrs()
+            f1 = self.f_fc1[l]
+            _lib.call("iw_linear8_gelu_frag", h8f.data_ptr(), *f1.args(), lut, im, is_, om, os_, ci, co,
+                      f8f.data_ptr(), B, f1.K, f1.N, f1.bias is not None, f1.wz is not None, True,
+                      _stream())
+            self.f_fc2[l].linear32_res(f8f, B, x16, sc["m"])
 
     def _replay(self, n: int):
         if n <= 0:

@@ -320,6 +320,79 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                int32_t timestamp_begin, int32_t max_initial_timestamp,
                                float logit_scale, iw_stream_t stream);
 
+/* -------------------------------------------------------------------------
+ * Fragment-major operands of the one-token decode step. No counterpart in
+ * the reference: an operand layout for the batched greedy step above, in
+ * which each int8 MFMA operand is one contiguous 1 KB piece so that a decode
+ * GEMM issues all of its loads at once. An int8 matrix X[R][K] is stored as
+ * [Rp/32][Kp/32][64][16] with Rp = R rounded up to 32 and Kp = K rounded up
+ * to a multiple of 320, K <= 5120: byte k of row r sits at
+ *   (r/32)*32*Kp + (k/32)*1024 + (r%32 + 32*((k/16)%2))*16 + k%16,
+ * and the padding holds zeros. Results equal the row-major entry points'.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of the fragment-major image of an int8 [rows][cols] matrix
+ * (0 for cols > 5120 or a negative size). */
+int64_t iw_frag_bytes(int64_t rows, int64_t cols);
+
+/* Row-major src [rows][cols] (row stride ld) to its fragment-major image,
+ * padding included (dst holds iw_frag_bytes(rows, cols) bytes). */
+int iw_frag_pack(const int8_t *src, int64_t rows, int64_t cols, int64_t ld, int8_t *dst,
+                 iw_stream_t stream);
+
+/* iw_linear8 / iw_linear8_gelu with x and weight fragment-major (M <= 128);
+ * out is row-major [M][N] or, when out_frag, the fragment-major image of
+ * [M][N]. */
+int iw_linear8_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                    const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                    int8_t *out, int64_t M, int64_t K, int64_t N, bool has_bias, bool asymmetric,
+                    bool out_frag, iw_stream_t stream);
+int iw_linear8_gelu_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                         const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
+                         const uint8_t *lut, const uint8_t *luti_multiplier, const int8_t *luti_shift,
+                         const uint8_t *luto_multiplier, const int8_t *luto_shift, int64_t luti_count,
+                         int64_t luto_count, int8_t *out, int64_t M, int64_t K, int64_t N,
+                         bool has_bias, bool asymmetric, bool out_frag, iw_stream_t stream);
+
+/* iw_linear32_residual15 with x and weight fragment-major (M <= 128). */
+int iw_linear32_residual15_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                                const int8_t *weight_zero, const uint32_t *multiplier,
+                                const int8_t *shift, const int16_t *residual,
+                                uint16_t residual_multiplier, int16_t *out, int64_t M, int64_t K,
+                                int64_t N, bool has_bias, bool asymmetric, iw_stream_t stream);
+
+/* iw_linear8_qkv_cache with x and weight fragment-major. */
+int iw_linear8_qkv_cache_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
+                              const int8_t *weight_zero, const uint32_t *multiplier,
+                              const int8_t *shift, int64_t M, int64_t K, bool has_bias,
+                              bool asymmetric, int8_t *q_out, int64_t q_ld, int8_t *k_cache,
+                              int64_t k_sb, int64_t k_sh, int64_t k_st, int8_t *v_cache,
+                              int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
+                              int64_t head_dim, int64_t tokens_per_row_group,
+                              int64_t cache_positions, const int32_t *pos, iw_stream_t stream);
+
+/* iw_layernorm32 writing the fragment-major image of out [rows][hidden]
+ * (rows <= 128). */
+int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *bias,
+                        uint8_t ln_multiplier, int8_t ln_shift, uint32_t out_multiplier,
+                        int8_t out_shift, uint32_t rsqrt_offset, int8_t *out, int64_t rows,
+                        int64_t hidden, bool has_bias, iw_stream_t stream);
+
+/* iw_attention_decode_cache writing the fragment-major image of out
+ * [batch][heads*head_dim] (batch <= 128, heads*head_dim <= 5120). */
+int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
+                                   int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
+                                   int64_t v_sh, int64_t v_sd, int8_t *out, int64_t batch,
+                                   int64_t heads, int64_t head_dim, int64_t k_length,
+                                   const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
+                                   int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
+                                   int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream);
+
+/* iw_classifier with x and weight fragment-major (M <= 128, K <= 5120); out
+ * row-major [M][N]. */
+int iw_classifier_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift,
+                       int8_t *out, int64_t M, int64_t K, int64_t N, iw_stream_t stream);
+
 /* Log-mel spectrogram (log_mel_spectrogram, audio.py:216-267, with N_FFT =
  * 512, HOP_LENGTH = 160): for each of `batch` rows of float32 audio
  * (n_samples > 256, row stride audio_ld) and frame t < n_samples / 160, the

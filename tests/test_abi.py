@@ -17,7 +17,7 @@ def _declarations():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     decls = {}
-    for m in re.finditer(r"\b(?:int|const char\s*\*)\s*(iw_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int64_t|int|const char\s*\*)\s*(iw_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         decls[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
     return decls
@@ -48,7 +48,8 @@ def test_library_exports_every_declared_function(lib):
 
 def test_binding_matches_header(iw):
     decls = _declarations()
-    sigs = iw._lib.SIGNATURES
+    sigs = dict(iw._lib.SIGNATURES)
+    sigs.update({name: argtypes for name, (argtypes, _) in iw._lib.VALUE_FUNCS.items()})
     assert set(sigs) | {"iw_abi_version", "iw_last_error"} == set(decls)
     for name, argtypes in sigs.items():
         assert len(argtypes) == decls[name], name
@@ -65,3 +66,13 @@ def test_validation_errors_reach_iw_last_error(iw, lib):
     assert b"unsupported LayerNorm hidden size" in lib.iw_last_error()
     lib.iw_abi_version.restype = ctypes.c_int
     assert lib.iw_abi_version() >= 1
+
+
+def test_frag_bytes(iw):
+    """Size of a fragment-major image: rows rounded up to 32, columns to 320."""
+    v = iw._lib.value
+    assert v("iw_frag_bytes", 128, 1280) == 128 * 1280
+    assert v("iw_frag_bytes", 5, 384) == 32 * 640
+    assert v("iw_frag_bytes", 33, 5120) == 64 * 5120
+    assert v("iw_frag_bytes", 51865, 1280) == 51872 * 1280
+    assert v("iw_frag_bytes", 1, 5121) == 0 and v("iw_frag_bytes", -1, 4) == 0

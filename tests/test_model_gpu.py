@@ -124,6 +124,24 @@ def test_greedy_decode_runner(iw, small, batch, steps):
     assert np.array_equal(host(toks), etoks)
 
 
+def test_greedy_decode_row_major_step(iw, small):
+    """The one-token step on row-major operands (DecoderRunner(frag=False), the
+    layer kernels of the prompt step) gives the oracle's logits and tokens too."""
+    dims, P, model, ref = small
+    batch, steps = 2, 6
+    mel = iw.synth.synthetic_mel(batch, dims.n_mels, 2 * dims.n_audio_ctx, seed=43)
+    prompt = gen.rng(7).integers(0, dims.n_vocab, size=(batch, 3)).astype(np.int64)
+    with torch.no_grad():
+        feats = model.embed_audio(T(mel))
+        runner = iw.DecoderRunner(model.decoder, batch, feats.shape[1], use_graph=False, frag=False)
+        assert not runner.frag
+        toks, logits = iw.greedy_decode(model, feats, T(prompt), steps, runner=runner, keep_logits=True)
+    xa = ref.encoder(mel)
+    etoks, elogits = ref.greedy(xa, prompt, steps, return_logits=True)
+    assert np.array_equal(host(logits), elogits)
+    assert np.array_equal(host(toks), etoks)
+
+
 def test_head_dim_96_and_128(iw, gpu):
     """Head sizes of the tiny (4 heads of 96) and the 10-head large-like shapes."""
     from oracle.model_oracle import OracleWhisper
