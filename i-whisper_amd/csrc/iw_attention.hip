@@ -708,6 +708,13 @@ __device__ __forceinline__ void lds_barrier() {
 #ifndef IW_DS_CH
 #define IW_DS_CH 128
 #endif
+// the self-attention instance (at most 512 keys) has its own ring shape
+#ifndef IW_DSS_NR
+#define IW_DSS_NR 3
+#endif
+#ifndef IW_DSS_CH
+#define IW_DSS_CH 128
+#endif
 
 template <int MAXK, int NR, int CH>
 __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
@@ -948,7 +955,7 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
     // (self-attention caches up to 512 positions get their own, smaller
     // instance, so profiles separate it from cross-attention)
     if (a.max_tk <= 512)
-      hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a, pos);
+      hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DSS_NR, IW_DSS_CH>), grid, dim3(256), 0, s, a, pos);
     else if (a.max_tk <= 2048)
       hipLaunchKernelGGL((attn_decode_stream_kernel<2048, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a, pos);
     else
