@@ -34,8 +34,51 @@ __device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
   return v;
 }
 
+// Wave-wide sum / max with DPP moves (no LDS round trips): xor-1 and xor-2
+// quad permutes, then the half-row and row mirrors give every lane its
+// 16-lane row's total; the four rows are added from lanes 0, 16, 32, 48.
+__device__ __forceinline__ uint32_t row16_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true);   // quad [1,0,3,2]
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true);   // quad [2,3,0,1]
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, true);  // row_half_mirror
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, true);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
+  v = row16_sum(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+}
+__device__ __forceinline__ int32_t wave_max_dpp(int32_t v) {
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0xB1, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x4E, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x141, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x140, 0xf, 0xf, false));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
 // LayerNorm32 (layernorm/layernorm_scalar.cpp:464-624), one wave per row.
 // The row lives in registers: lane l owns 4-element chunks l, l + 64, ...
+// The waves are persistent: each loads its lanes' gamma / beta once, then
+// walks the rows wave_id, wave_id + waves, ..., requesting the next row
+// before reducing the current one.
+//
+// The integer steps are the reference's; their arithmetic is arranged for
+// the VALU, which bounds this kernel at encoder sizes:
+// * one pass over the raw int16 pairs gives the sum (v_dot2 with ones) and
+//   the row's largest and smallest value (packed max / min), reduced
+//   together with DPP moves;
+// * max_e int32(d_e^2), d = x - mean, is max(xmax - mean, mean - xmin)^2
+//   whenever every |d| <= 46340 (then no d^2 wraps, and d^2 grows with |d|);
+//   a row outside that range takes the per-element form;
+// * d^2 and the (non-negative) rounding shift of the variance sum use 24-bit
+//   multiply-adds; d * inv * ln_m is d * K with K = inv * ln_m (mod 2^32)
+//   formed once per row (written as two 24-bit products, which the compiler
+//   may fuse back into one 32-bit multiply), and mulh is a signed high
+//   multiply with a mask correction for multipliers >= 2^31.
 constexpr int LN_MAX_CHUNKS = 5;  // 1280 / 4 / 64
 
 __global__ __launch_bounds__(256) void layernorm32_kernel(
@@ -44,12 +87,20 @@ __global__ __launch_bounds__(256) void layernorm32_kernel(
     int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int64_t rows, int hidden,
     int code) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int nch = hidden >> 2;
-  const int16_t *xr = x + row * hidden;
-  // gamma / beta of this lane's columns are requested with the row, so their
-  // latency hides behind the reductions
+  const int64_t wave_id = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t waves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  if (wave_id >= rows) return;
+  const int nch = hidden >> 2;  // >= 96: every lane owns chunk 0
+  auto load_row = [&](int64_t r, uint2 *w) {
+    const int16_t *xr = x + r * hidden;
+#pragma unroll
+    for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+      const int ch = lane + 64 * c;
+      w[c] = ch < nch ? *reinterpret_cast<const uint2 *>(xr + ch * 4) : make_uint2(0, 0);
+    }
+  };
+  uint2 xa[LN_MAX_CHUNKS];
+  load_row(wave_id, xa);
   const bool g_al = (reinterpret_cast<uintptr_t>(gamma) & 3) == 0;
   const bool b_al = beta && (reinterpret_cast<uintptr_t>(beta) & 15) == 0;
   uint32_t gw[LN_MAX_CHUNKS];
@@ -74,95 +125,113 @@ __global__ __launch_bounds__(256) void layernorm32_kernel(
       }
     }
   }
-  int32_t v[LN_MAX_CHUNKS][4];
-  uint32_t sum = 0;
+  // rshift by out_s: a shift >= 32 (or negative) gives 0, as a zero multiplier does
+  const bool out_zero = (uint32_t)out_s >= 32;
+  const uint32_t om = out_zero ? 0u : out_m;
+  const uint32_t osh = out_zero ? 0u : (uint32_t)out_s;
+  const uint32_t omneg = (uint32_t)((int32_t)om >> 31);
+  const s16x2 ones = {1, 1};
+  // one row: xw holds its raw values on entry and is refilled with row
+  // `next` (if any) as soon as they are unpacked
+  auto process = [&](int64_t row, uint2 *xw, int64_t next) {
+    int32_t sum = 0;
+    s16x2 mx2 = {-32768, -32768}, mn2 = {32767, 32767};
 #pragma unroll
-  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < nch) {
-      const uint2 w = *reinterpret_cast<const uint2 *>(xr + ch * 4);
-      v[c][0] = (int16_t)(w.x & 0xffff);
-      v[c][1] = (int16_t)(w.x >> 16);
-      v[c][2] = (int16_t)(w.y & 0xffff);
-      v[c][3] = (int16_t)(w.y >> 16);
-      sum += (uint32_t)(v[c][0] + v[c][1] + v[c][2] + v[c][3]);
+    for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+      if (lane + 64 * c < nch) {
+        const s16x2 p0 = __builtin_bit_cast(s16x2, xw[c].x), p1 = __builtin_bit_cast(s16x2, xw[c].y);
+        sum = __builtin_amdgcn_sdot2(p0, ones, sum, false);
+        sum = __builtin_amdgcn_sdot2(p1, ones, sum, false);
+        mx2 = __builtin_elementwise_max(mx2, __builtin_elementwise_max(p0, p1));
+        mn2 = __builtin_elementwise_min(mn2, __builtin_elementwise_min(p0, p1));
+      }
+    }
+    int32_t v[LN_MAX_CHUNKS][4];
+#pragma unroll
+    for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+      v[c][0] = (int16_t)(xw[c].x & 0xffff);
+      v[c][1] = (int16_t)(xw[c].x >> 16);
+      v[c][2] = (int16_t)(xw[c].y & 0xffff);
+      v[c][3] = (int16_t)(xw[c].y >> 16);
+    }
+    if (next < rows) load_row(next, xw);
+    const int32_t total = (int32_t)wave_sum_dpp((uint32_t)sum);
+    const int32_t xmax = wave_max_dpp(max((int32_t)mx2.x, (int32_t)mx2.y));
+    const int32_t xmin = -wave_max_dpp(-min((int32_t)mn2.x, (int32_t)mn2.y));
+    const int32_t mean = norm_reduce(total, code);
+#pragma unroll
+    for (int c = 0; c < LN_MAX_CHUNKS; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[c][e] -= mean;  // d
+    const int32_t maxabs = max(xmax - mean, mean - xmin);
+    const bool fast = maxabs <= 46340;  // wave-uniform
+    int32_t maxsq;
+    if (fast) {
+      maxsq = maxabs * maxabs;
     } else {
-      v[c][0] = v[c][1] = v[c][2] = v[c][3] = 0;
+      maxsq = 0;
+#pragma unroll
+      for (int c = 0; c < LN_MAX_CHUNKS; ++c)
+        if (lane + 64 * c < nch)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) maxsq = max(maxsq, (int32_t)((uint32_t)v[c][e] * (uint32_t)v[c][e]));
+      maxsq = wave_max_dpp(maxsq);
     }
-  }
-  const int32_t mean = norm_reduce((int32_t)wave_sum_u32(sum), code);
-  int32_t maxsq = 0;
+    int32_t rs = bitlen(maxsq) - 16;
+    rs = rs < 0 ? 0 : rs;
+    rs = (rs + 1) & ~1;
+    uint32_t vs = 0;
+    if (fast) {
+      // d^2 < 2^31 and rs <= 16: rshift of a non-negative value, no wrap
+      const int32_t half = rs ? 1 << (rs - 1) : 0;
 #pragma unroll
-  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
-    if (lane + 64 * c < nch) {
+      for (int c = 0; c < LN_MAX_CHUNKS; ++c)
+        if (lane + 64 * c < nch)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int32_t d = v[c][e] - mean;
-        maxsq = max(maxsq, (int32_t)((uint32_t)d * (uint32_t)d));
+          for (int e = 0; e < 4; ++e) vs += (uint32_t)(__mul24(v[c][e], v[c][e]) + half) >> rs;
+    } else {
+#pragma unroll
+      for (int c = 0; c < LN_MAX_CHUNKS; ++c)
+        if (lane + 64 * c < nch)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            vs += (uint32_t)rshift((int32_t)((uint32_t)v[c][e] * (uint32_t)v[c][e]), (uint32_t)rs);
+    }
+    const int32_t var = norm_reduce((int32_t)wave_sum_dpp(vs), code);
+    const int32_t inv = fisr(var, rsqrt_off);
+    // t = d * inv * ln_m modulo 2^32 = d * K; a shift >= 32 gives 0 (K = 0)
+    uint32_t nshift = (uint32_t)(ln_s + (rs >> 1));
+    uint32_t K = (uint32_t)inv * ln_m;
+    if (nshift >= 32) K = 0, nshift = 0;
+    const int32_t klo = (int32_t)(K & 0xffffu), khi = (int32_t)(K >> 16);
+    const uint32_t nhalf = nshift ? 1u << (nshift - 1) : 0u, nw = min(nshift, 1u);
+    const uint32_t ohalf = osh ? 1u << (osh - 1) : 0u, ow = min(osh, 1u);
+    int8_t *orow = out + row * hidden;
+#pragma unroll
+    for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < nch) {
+        uint32_t packed = 0;
+        const uint32_t bv[4] = {bw[c].x, bw[c].y, bw[c].z, bw[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int32_t d = v[c][e];  // |d| < 2^17: exact in the 24-bit multiplier
+          const uint32_t t = (uint32_t)__mul24(d, klo) + ((uint32_t)__mul24(d, khi) << 16);
+          const uint32_t ts = (uint32_t)__builtin_amdgcn_sbfe((int32_t)t, 31, nw);
+          const int32_t y = clampi((int32_t)(t + nhalf + ts) >> nshift, -16383, 16383);
+          const uint32_t a = (uint32_t)__mul24(y, (int32_t)(int8_t)(gw[c] >> (8 * e))) + bv[e];
+          // mulh(a, om): signed high word, plus a when om >= 2^31
+          const uint32_t hi = (uint32_t)__mulhi((int32_t)a, (int32_t)om) + (a & omneg);
+          const uint32_t hs = (uint32_t)__builtin_amdgcn_sbfe((int32_t)hi, 31, ow);
+          const int32_t o = clampi((int32_t)(hi + ohalf + hs) >> osh, -127, 127);
+          packed |= ((uint32_t)(uint8_t)(int8_t)o) << (8 * e);
+        }
+        *reinterpret_cast<uint32_t *>(orow + ch * 4) = packed;
       }
     }
-  }
-  maxsq = wave_max_i32(maxsq);
-  int32_t rs = bitlen(maxsq) - 16;
-  rs = rs < 0 ? 0 : rs;
-  rs = (rs + 1) & ~1;
-  uint32_t vs = 0;
-#pragma unroll
-  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
-    if (lane + 64 * c < nch) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int32_t d = v[c][e] - mean;
-        vs += (uint32_t)rshift((int32_t)((uint32_t)d * (uint32_t)d), (uint32_t)rs);
-      }
-    }
-  }
-  const int32_t var = norm_reduce((int32_t)wave_sum_u32(vs), code);
-  const int32_t inv = fisr(var, rsqrt_off);
-  const uint32_t nshift = (uint32_t)(ln_s + (rs >> 1));
-  int8_t *orow = out + row * hidden;
-#pragma unroll
-  for (int c = 0; c < LN_MAX_CHUNKS; ++c) {
-    const int ch = lane + 64 * c;
-    if (ch < nch) {
-      uint32_t packed = 0;
-      const uint32_t bv[4] = {bw[c].x, bw[c].y, bw[c].z, bw[c].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int32_t d = v[c][e] - mean;
-        uint32_t t = (uint32_t)d * (uint32_t)inv * ln_m;
-        int32_t y = clampi(rshift((int32_t)t, nshift), -16383, 16383);
-        uint32_t a = (uint32_t)y * (uint32_t)(int32_t)(int8_t)(gw[c] >> (8 * e)) + bv[e];
-        int32_t o = clampi(rshift(mulh((int32_t)a, out_m), (uint32_t)out_s), -127, 127);
-        packed |= ((uint32_t)(uint8_t)(int8_t)o) << (8 * e);
-      }
-      *reinterpret_cast<uint32_t *>(orow + ch * 4) = packed;
-    }
-  }
-}
-
-// Wave-wide sum / max with DPP moves (no LDS round trips): xor-1 and xor-2
-// quad permutes, then the half-row and row mirrors give every lane its
-// 16-lane row's total; the four rows are added from lanes 0, 16, 32, 48.
-__device__ __forceinline__ uint32_t row16_sum(uint32_t v) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true);   // quad [1,0,3,2]
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true);   // quad [2,3,0,1]
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, true);  // row_half_mirror
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, true);  // row_mirror
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
-  v = row16_sum(v);
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
-         (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-}
-__device__ __forceinline__ int32_t wave_max_dpp(int32_t v) {
-  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0xB1, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x4E, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x141, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x140, 0xf, 0xf, false));
-  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+  };
+  // rows wave_id + k * waves, the next one in flight
+  for (int64_t row = wave_id; row < rows; row += waves) process(row, xa, row + waves);
 }
 
 // LayerNorm32 for few rows (a decode step): one row per block of 256 threads,
@@ -601,6 +670,23 @@ int grid_for(int64_t n, int threads) {
 // row counts up to which each row gets a block of its own
 constexpr int64_t kLnRowBlockMaxRows = 2048;
 
+// Blocks of layernorm32_kernel resident on the whole device at once (its
+// persistent grid): CUs x blocks per CU at the kernel's register use.
+int64_t ln_persistent_blocks() {
+  static const int64_t blocks = [] {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, layernorm32_kernel, 256, 0) != hipSuccess ||
+        cus <= 0 || per_cu <= 0) {
+      (void)hipGetLastError();
+      return (int64_t)256 * 4;
+    }
+    return (int64_t)cus * per_cu;
+  }();
+  return blocks;
+}
+
 int layernorm_width_code(int64_t h) {
   switch (h) {
     case 384: return 0;
@@ -626,8 +712,9 @@ int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *bet
                        code, out_frag ? frag_kpad(hidden) : (int64_t)0);
     return check_launch("layernorm32_row_kernel");
   }
-  // one row per wave, four rows per block
-  const int64_t blocks = (rows + 3) / 4;
+  // one row per wave at a time, four waves per block; persistent waves, as
+  // many blocks as the device holds at once
+  const int64_t blocks = std::min<int64_t>((rows + 3) / 4, ln_persistent_blocks());
   hipLaunchKernelGGL(layernorm32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, gamma, beta,
                      (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, rows,
                      (int)hidden, code);
