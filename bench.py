@@ -132,6 +132,76 @@ def cross_attention_probe(dec, dims, batch: int, launches: int = 20) -> float:
     return sum(e0.elapsed_time(e1) for e0, e1 in ev) / launches
 
 
+def rowop_bandwidth(iw, rows: int, channels: int, batch: int, positions: int, reps: int = 10) -> dict:
+    """HBM rate of the row / elementwise kernels at the encoder's activation
+    sizes, each launched alone (HIP events around `reps` launches on the
+    current stream): the LayerNorm every encoder block runs twice, and the
+    op-level GeLU (FC1-sized input), residual15 and add_requant15 kernels
+    (the model path fuses the last three into GEMM epilogues). Bytes are the
+    algorithmic ones: every input read once, every output written once."""
+    import torch
+
+    L = iw._lib
+    st = torch.cuda.current_stream().cuda_stream
+    dev = "cuda"
+
+    def timed(fn) -> float:
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    n = rows * channels
+    out = {}
+
+    def report(name, ms, nbytes):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes,
+                     "avg_launch_ms": round(ms, 4)}
+
+    x16 = torch.randint(-16383, 16384, (rows, channels), dtype=torch.int16, device=dev, generator=g)
+    gam = torch.randint(-127, 128, (channels,), dtype=torch.int8, device=dev, generator=g)
+    bet = torch.randint(-4096, 4096, (channels,), dtype=torch.int32, device=dev, generator=g)
+    o8 = torch.empty((rows, channels), dtype=torch.int8, device=dev)
+    ms = timed(lambda: L.call("iw_layernorm32", x16.data_ptr(), gam.data_ptr(), bet.data_ptr(), 200, 10, 1 << 31,
+                              5, 13, o8.data_ptr(), rows, channels, True, st))
+    report("layernorm32_kernel", ms, 3 * n)
+    del o8
+    f = 4 * channels
+    x8 = torch.randint(-127, 128, (rows, f), dtype=torch.int8, device=dev, generator=g)
+    y8 = torch.empty_like(x8)
+    lut = torch.randint(0, 256, (16,), dtype=torch.int32, device=dev, generator=g).to(torch.uint8)
+    pm = torch.randint(1, 256, (f,), dtype=torch.int32, device=dev, generator=g).to(torch.uint8)
+    ps = torch.randint(4, 12, (f,), dtype=torch.int8, device=dev, generator=g)
+    ms = timed(lambda: L.call("iw_gelu", x8.data_ptr(), lut.data_ptr(), pm.data_ptr(), ps.data_ptr(), pm.data_ptr(),
+                              ps.data_ptr(), y8.data_ptr(), rows * f, f, f, f, st))
+    report("gelu16_kernel", ms, 2 * rows * f)
+    del x8, y8
+    br = torch.randint(-2 ** 30, 2 ** 30, (rows, channels), dtype=torch.int32, device=dev, generator=g)
+    r16 = torch.empty_like(x16)
+    ms = timed(lambda: L.call("iw_residual15", br.data_ptr(), x16.data_ptr(), 1234, r16.data_ptr(), n, st))
+    report("residual15_kernel", ms, 8 * n)
+    del br
+    xe = torch.randint(-127, 128, (rows, channels), dtype=torch.int8, device=dev, generator=g)
+    pe = torch.randint(-127, 128, (positions, channels), dtype=torch.int8, device=dev, generator=g)
+    m16 = torch.full((channels,), 300, dtype=torch.int16, device=dev)
+    s8 = torch.full((channels,), 6, dtype=torch.int8, device=dev)
+    ms = timed(lambda: L.call("iw_add_requant15", xe.data_ptr(), pe.data_ptr(), m16.data_ptr(), s8.data_ptr(),
+                              r16.data_ptr(), batch, positions, channels, channels, channels, st))
+    report("add_requant15_16_kernel", ms, 3 * n + positions * channels)
+    del xe, pe, r16, x16
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,6 +272,7 @@ def main():
         wall = time.perf_counter() - t_start
         if dsteps:
             xa_ms = cross_attention_probe(dec, dims, batch)
+        rowops = rowop_bandwidth(iw, batch * dims.n_audio_ctx, dims.n_audio_state, batch, dims.n_audio_ctx)
     enc_ms = sum(e0.elapsed_time(e1) for e0, e1, _, _ in evs)
     dec_ms = sum(e1.elapsed_time(e2) for _, e1, e2, _ in evs)
     K = args.steps
@@ -240,6 +311,7 @@ def main():
             "achieved": round(g_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
             "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": recorded_traffic(GEMM_TRAFFIC_KEY),
             "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4)},
+        "hbm_kernels": rowops,
     }
     if dsteps:
         # algorithmic bytes: K [Tk, D] and V [D, Tk] of every (b, h), q and out

@@ -363,6 +363,129 @@ __global__ void add_requant15_kernel(const int8_t *__restrict__ x, const int64_t
   }
 }
 
+// Vector forms of the two elementwise kernels above for rows of a multiple
+// of 16 channels and 16-byte aligned operands: each thread takes 16
+// consecutive elements of one row (16-byte loads and stores), reads the
+// per-channel parameters as 16-channel vectors, and walks the grid with
+// running (row, channel) counters instead of a division per element.
+struct PieceWalk {
+  int64_t p, row;
+  uint32_t c;  // piece within the row
+  int64_t drow;
+  uint32_t dc, cp;
+  __device__ PieceWalk(int64_t start, int64_t stride, uint32_t cpieces) {
+    p = start;
+    row = start / cpieces;
+    c = (uint32_t)(start % cpieces);
+    drow = stride / cpieces;
+    dc = (uint32_t)(stride % cpieces);
+    cp = cpieces;
+  }
+  // returns the number of rows advanced
+  __device__ int64_t next(int64_t stride) {
+    p += stride;
+    c += dc;
+    int64_t adv = drow;
+    if (c >= cp) c -= cp, ++adv;
+    row += adv;
+    return adv;
+  }
+};
+
+__device__ __forceinline__ uint32_t byte_of(const uint4 &v, int i) {
+  const uint32_t w = i < 4 ? v.x : (i < 8 ? v.y : (i < 12 ? v.z : v.w));
+  return (w >> (8 * (i & 3))) & 0xffu;
+}
+
+__global__ __launch_bounds__(256) void gelu16_kernel(const int8_t *__restrict__ x, const uint8_t *__restrict__ lut,
+                                                     const uint8_t *__restrict__ luti_m,
+                                                     const int8_t *__restrict__ luti_s,
+                                                     const uint8_t *__restrict__ luto_m,
+                                                     const int8_t *__restrict__ luto_s, int8_t *__restrict__ out,
+                                                     int64_t pieces, uint32_t cpieces, int luti_pc, int luto_pc) {
+  __shared__ uint8_t sl[16];
+  if (threadIdx.x < 16) sl[threadIdx.x] = lut[threadIdx.x];
+  __syncthreads();
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t start = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (start >= pieces) return;
+  // per-tensor parameters as broadcast vectors
+  const uint4 bim = make_uint4(luti_m[0] * 0x01010101u, 0, 0, 0), bis = make_uint4((uint8_t)luti_s[0] * 0x01010101u, 0, 0, 0);
+  const uint4 bom = make_uint4(luto_m[0] * 0x01010101u, 0, 0, 0), bos = make_uint4((uint8_t)luto_s[0] * 0x01010101u, 0, 0, 0);
+  for (PieceWalk w(start, stride, cpieces); w.p < pieces; w.next(stride)) {
+    const uint4 xv = *reinterpret_cast<const uint4 *>(x + w.p * 16);
+    const int64_t c0 = (int64_t)w.c * 16;
+    const uint4 im = luti_pc ? *reinterpret_cast<const uint4 *>(luti_m + c0) : bim;
+    const uint4 is = luti_pc ? *reinterpret_cast<const uint4 *>(luti_s + c0) : bis;
+    const uint4 om = luto_pc ? *reinterpret_cast<const uint4 *>(luto_m + c0) : bom;
+    const uint4 os = luto_pc ? *reinterpret_cast<const uint4 *>(luto_s + c0) : bos;
+    uint32_t o[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int pi = luti_pc ? i : 0, po = luto_pc ? i : 0;
+      const int8_t y = gelu_one((int8_t)byte_of(xv, i), sl, byte_of(im, pi), (int8_t)byte_of(is, pi),
+                                byte_of(om, po), (int8_t)byte_of(os, po));
+      o[i >> 2] |= (uint32_t)(uint8_t)y << (8 * (i & 3));
+    }
+    *reinterpret_cast<uint4 *>(out + w.p * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void add_requant15_16_kernel(
+    const int8_t *__restrict__ x, const int64_t *__restrict__ tokens, const int8_t *__restrict__ addend,
+    const uint16_t *__restrict__ mult, const int8_t *__restrict__ shift, int16_t *__restrict__ out,
+    int64_t positions, int64_t channels, int64_t pieces, int mpc, int spc, const int32_t *__restrict__ pos,
+    int64_t addend_rows) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t start = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (start >= pieces) return;
+  const int64_t p0 = pos ? min(max((int64_t)*pos, (int64_t)0), addend_rows - positions) : 0;
+  const uint32_t cpieces = (uint32_t)(channels / 16);
+  const uint32_t m0 = mult[0];
+  const int32_t s0 = shift[0];
+  PieceWalk w(start, stride, cpieces);
+  // t = row % positions, kept as a running counter too
+  int64_t t = w.row % positions;
+  const int64_t dt = w.drow % positions;
+  for (; w.p < pieces;) {
+    const int64_t c0 = (int64_t)w.c * 16;
+    const int8_t *xr = tokens ? x + tokens[w.row] * channels + c0 : x + w.p * 16;
+    const uint4 xv = *reinterpret_cast<const uint4 *>(xr);
+    const uint4 av = *reinterpret_cast<const uint4 *>(addend + (t + p0) * channels + c0);
+    uint4 mv0 = make_uint4(0, 0, 0, 0), mv1 = mv0, sv = mv0;
+    if (mpc) {
+      mv0 = *reinterpret_cast<const uint4 *>(mult + c0);
+      mv1 = *reinterpret_cast<const uint4 *>(mult + c0 + 8);
+    }
+    if (spc) sv = *reinterpret_cast<const uint4 *>(shift + c0);
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int32_t v = (int32_t)(int8_t)byte_of(xv, i) + (int32_t)(int8_t)byte_of(av, i);
+      uint32_t m = m0;
+      if (mpc) {
+        const uint4 &mv = i < 8 ? mv0 : mv1;
+        const int j = i & 7;
+        const uint32_t ww = j < 2 ? mv.x : (j < 4 ? mv.y : (j < 6 ? mv.z : mv.w));
+        m = (ww >> (16 * (j & 1))) & 0xffffu;
+      }
+      const int32_t sh = spc ? (int32_t)(int8_t)byte_of(sv, i) : s0;
+      const int32_t pr = (int32_t)((uint32_t)v * m);
+      const uint32_t r = (uint32_t)(uint16_t)(int16_t)clampi(rshift(pr, (uint32_t)(sh < 0 ? 0 : sh)), -16383, 16383);
+      if (i & 1)
+        o[i >> 1] |= r << 16;
+      else
+        o[i >> 1] = r;
+    }
+    uint4 *op = reinterpret_cast<uint4 *>(out + w.p * 16);
+    op[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    op[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    const int64_t adv = w.next(stride);
+    t += dt + (adv - w.drow);  // adv is drow or drow + 1
+    if (t >= positions) t -= positions;
+  }
+}
+
 // Encoder input quantization round(mel * alpha) clamped to +-127
 // (model_int.py:1265-1267; round half to even as torch.round), written
 // channels-last [B][T][n_mels] for the implicit-GEMM conv.
@@ -732,6 +855,15 @@ int launch_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_m, cons
                 const uint8_t *luto_m, const int8_t *luto_s, int8_t *out, int64_t numel,
                 int64_t channels, int luti_pc, int luto_pc, hipStream_t s) {
   if (numel == 0) return 0;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                       (luti_pc ? reinterpret_cast<uintptr_t>(luti_m) | reinterpret_cast<uintptr_t>(luti_s) : 0) |
+                       (luto_pc ? reinterpret_cast<uintptr_t>(luto_m) | reinterpret_cast<uintptr_t>(luto_s) : 0);
+  if (channels % 16 == 0 && numel % channels == 0 && (al & 15) == 0 && channels / 16 <= 0xffffffffLL) {
+    const int64_t pieces = numel / 16;
+    hipLaunchKernelGGL(gelu16_kernel, dim3(grid_for(pieces, 256)), dim3(256), 0, s, x, lut, luti_m, luti_s,
+                       luto_m, luto_s, out, pieces, (uint32_t)(channels / 16), luti_pc, luto_pc);
+    return check_launch("gelu16_kernel");
+  }
   hipLaunchKernelGGL(gelu_kernel, dim3(grid_for(numel, 256)), dim3(256), 0, s, x, lut, luti_m,
                      luti_s, luto_m, luto_s, out, numel, channels, luti_pc, luto_pc);
   return check_launch("gelu_kernel");
@@ -751,6 +883,15 @@ int launch_add_requant15(const int8_t *x, const int64_t *tokens, const int8_t *a
                          const int32_t *pos, int64_t addend_rows) {
   const int64_t total = batch * positions * channels;
   if (total == 0) return 0;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(addend) |
+                       reinterpret_cast<uintptr_t>(out) | (mpc ? reinterpret_cast<uintptr_t>(mult) : 0) |
+                       (spc ? reinterpret_cast<uintptr_t>(shift) : 0);
+  if (channels % 16 == 0 && (al & 15) == 0 && channels / 16 <= 0xffffffffLL) {
+    const int64_t pieces = total / 16;
+    hipLaunchKernelGGL(add_requant15_16_kernel, dim3(grid_for(pieces, 256)), dim3(256), 0, s, x, tokens, addend,
+                       mult, shift, out, positions, channels, pieces, mpc, spc, pos, addend_rows);
+    return check_launch("add_requant15_16_kernel");
+  }
   hipLaunchKernelGGL(add_requant15_kernel, dim3(grid_for(total, 256)), dim3(256), 0, s, x, tokens,
                      addend, mult, shift, out, positions, channels, total, mpc, spc, pos, addend_rows);
   return check_launch("add_requant15_kernel");
