@@ -193,6 +193,29 @@ def test_layernorm32(iw, oracle, gpu, hidden, rows, spread):
     assert np.array_equal(host(got), exp)
 
 
+@pytest.mark.parametrize("hidden", [384, 1280])
+@pytest.mark.parametrize("rows", [6, 2100])
+def test_layernorm32_full_int16_range(iw, oracle, gpu, hidden, rows):
+    """Rows whose deviations from the mean exceed 46340, where d^2 wraps in int32
+    (the kernels' per-element form), next to ordinary rows in the same launch:
+    one row-per-block launch (<= 2048 rows) and one persistent-wave launch."""
+    _print_case("layernorm32 full int16 range", hidden, rows)
+    x, g, b, lm, ls, om, os_ = gen.ln_case(hidden + rows + 1, rows, hidden, 3000)
+    r = gen.rng(rows)
+    x[0] = 32767
+    x[0, 5] = -32768                                     # one deviation of ~65000
+    x[1] = np.where(np.arange(hidden) % 2 == 0, -32768, 32767)  # |d| ~ 32767, no wrap
+    x[2] = r.integers(-32768, 32768, size=hidden)        # the full range
+    x[3] = -32768
+    x[3, -1] = 32767
+    x[rows // 2] = 30000
+    x[rows // 2, ::7] = -30000
+    got = iw.kernels.layernorm32_hip(
+        T(x), T(g), T(b), torch.tensor([lm], dtype=torch.uint8), torch.tensor([ls], dtype=torch.int8),
+        torch.tensor([om], dtype=torch.uint32), torch.tensor([os_], dtype=torch.int8))
+    assert np.array_equal(host(got), oracle.layernorm32(x, g, b, lm, ls, om, os_))
+
+
 @pytest.mark.parametrize("rows", [3, 5000])
 def test_layernorm32_unaligned_params(iw, oracle, gpu, rows):
     """gamma / beta views at odd offsets, and no beta at all."""
