@@ -87,6 +87,25 @@ def test_attention_decode_cache_wrap_corner(iw, oracle, gpu):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("wrap_head", [0, 1])
+@pytest.mark.parametrize("B,H,Tk,tcap", [(1, 2, 700, 1024), (3, 4, 1500, 1500), (2, 2, 40, 448)])
+def test_attention_decode_cache_heads_share_a_block(iw, oracle, gpu, wrap_head, B, H, Tk, tcap):
+    """Cross-attention-sized caches run two heads per block as one stream: each
+    head's row maximum, P, sums and wrap flag must stay its own. One head of
+    every pair takes the int16 row-max wrap (P = 128), the other does not."""
+    print("case: heads share a block", wrap_head, B, H, Tk, tcap, flush=True)
+    D = 64
+    q, k, v, qm, qs, f, am, as_ = gen.attn_case(11 * B + H + Tk, B, H, 1, Tk, D)
+    for h in range(wrap_head, H, 2):
+        q[:, h] = 127
+        k[:, h] = 127
+        k[:, h, 1::3] = -128
+    qm, qs, f = 255, 0, 8
+    exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
+    got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=Tk, pos_val=None, max_keys=Tk)
+    assert np.array_equal(got, exp)
+
+
 @pytest.mark.parametrize("B,Tn,H,D,pos_val,tcap", [(1, 1, 2, 64, 0, 448), (5, 1, 2, 64, 7, 448),
                                                     (128, 1, 2, 64, 100, 448), (4, 3, 2, 64, 0, 448),
                                                     (2, 3, 4, 32, 38, 40), (40, 3, 2, 64, 5, 448)])
