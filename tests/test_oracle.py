@@ -160,6 +160,22 @@ def test_shift_exp_all_inputs_vs_ref(oracle, ref):
             assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
 
 
+def test_shift_exp_table_clamp_is_exact(oracle):
+    """The fused attention kernels map a score to P through a 32768-entry table
+    indexed by min((row_max + 1 - score) mod 2^16, 32767). That equals the
+    reference's shift-exponential of every int16 difference, for every legal
+    frac_bits, because P is 0 from index 22796 on (and for the positive
+    differences above 32768 that the int16 wrap produces)."""
+    qk = np.arange(-32768, 32768, dtype=np.int16).reshape(1, 1, 1, -1)
+    zero = np.zeros((1, 1, 1, 1), np.int16)
+    for f in range(1, 14):
+        p = oracle.shift_exp(qk, zero, None, f)[0].reshape(-1)  # p[x + 32768] = P(x - 0)
+        table = p[32768 - np.arange(32768)]                      # table[i] = P(-i)
+        idx = (-qk.reshape(-1).astype(np.int64)) & 0xFFFF
+        assert np.array_equal(table[np.minimum(idx, 32767)], p), f
+        assert not table[22796:].any(), f
+
+
 def test_pv_negative_row_sum_raises(oracle, ref):
     p = np.zeros((1, 1, 1, 4), np.uint8)
     v = np.zeros((1, 1, 2, 4), np.int8)
