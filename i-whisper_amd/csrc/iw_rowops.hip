@@ -749,6 +749,40 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(
   }
 }
 
+// transpose_heads_kernel with 16-byte accesses (row strides, offsets and
+// H * D multiples of 16): a 64 x 64 tile is read as 16-byte row pieces into
+// LDS, and each thread writes 16 consecutive positions t of one feature
+// column (a byte gather down the tile); positions past T are not written.
+__global__ __launch_bounds__(256) void transpose_heads16_kernel(
+    const int8_t *__restrict__ src, int64_t src_sb, int64_t src_st, int8_t *__restrict__ dst,
+    int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off, int64_t T, int64_t H,
+    int64_t D) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[64][64 + 16];
+  const int64_t b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.x * 64;
+  const int64_t c0 = (int64_t)blockIdx.y * 64;  // feature column h*D + d
+  const int64_t C = H * D;
+  const int tid = threadIdx.x, r = tid >> 2, q = (tid & 3) * 16;
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (t0 + r < T && c0 + q < C) v = *reinterpret_cast<const uint4 *>(src + b * src_sb + (t0 + r) * src_st + c0 + q);
+  *reinterpret_cast<uint4 *>(&tile[r][q]) = v;
+  __syncthreads();
+  const int64_t c = c0 + r, t = t0 + q;
+  if (c >= C || t >= T) return;
+  uint32_t w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    w[k] = (uint32_t)tile[q + 4 * k][r] | ((uint32_t)tile[q + 4 * k + 1][r] << 8) |
+           ((uint32_t)tile[q + 4 * k + 2][r] << 16) | ((uint32_t)tile[q + 4 * k + 3][r] << 24);
+  const int32_t h = (int32_t)c / (int32_t)D, d = (int32_t)c - h * (int32_t)D;
+  int8_t *o = dst + b * dst_sb + (int64_t)h * dst_sh + (int64_t)d * dst_sd + t_off + t;
+  if (t + 16 <= T) {
+    *reinterpret_cast<uint4 *>(o) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    for (int i = 0; i < 16 && t + i < T; ++i) o[i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+  }
+}
+
 // Per-head gather of a [B, T, H*D] operand slice into a [B, H, T_cap, D]
 // cache at positions [t_off, t_off + T): dst[b*dst_sb + h*dst_sh + (t_off+t)*dst_st + d]
 // = src[b*src_sb + t*src_st + h*D + d], 16 bytes per thread (D % 16 == 0).
@@ -911,6 +945,14 @@ int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, in
                            int64_t B, int64_t T, int64_t H, int64_t D, hipStream_t s) {
   if (B * T * H * D == 0) return 0;
   const dim3 grid((unsigned)((T + 63) / 64), (unsigned)((H * D + 63) / 64), (unsigned)B);
+  const uintptr_t al = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | (uintptr_t)src_sb |
+                       (uintptr_t)src_st | (uintptr_t)dst_sb | (uintptr_t)dst_sh | (uintptr_t)dst_sd |
+                       (uintptr_t)t_off | (uintptr_t)(H * D);
+  if ((al & 15) == 0 && H * D <= 0x7fffffff) {
+    hipLaunchKernelGGL(transpose_heads16_kernel, grid, dim3(256), 0, s, src, src_sb, src_st, dst, dst_sb, dst_sh,
+                       dst_sd, t_off, T, H, D);
+    return check_launch("transpose_heads16_kernel");
+  }
   hipLaunchKernelGGL(transpose_heads_kernel, grid, dim3(256), 0, s, src, src_sb, src_st, dst,
                      dst_sb, dst_sh, dst_sd, t_off, T, H, D);
   return check_launch("transpose_heads_kernel");

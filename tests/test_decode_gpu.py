@@ -22,6 +22,9 @@ def T(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+T_ = T
+
+
 def host(t):
     return t.cpu().numpy()
 
@@ -138,6 +141,26 @@ def test_linear8_qkv_cache(iw, oracle, gpu, B, Tn, H, D, pos_val, tcap):
             vexp[:, :, :, t] = e[:, i, 2]
     assert np.array_equal(host(kc), kexp)
     assert np.array_equal(host(vc), vexp)
+
+
+@pytest.mark.parametrize("B,T,H,D,t_off", [(2, 1500, 4, 64, 0), (1, 37, 2, 64, 16), (3, 64, 3, 32, 0),
+                                           (2, 100, 2, 64, 3), (1, 5, 2, 48, 0)])
+def test_transpose_heads(iw, gpu, B, T, H, D, t_off):
+    """V of a fused [B, T, 3C] projection into per-head transposed [B, H, D, Tcap]
+    rows at positions t_off .. t_off + T; every other byte is left as it was."""
+    print("case: transpose heads", B, T, H, D, t_off, flush=True)
+    C = H * D
+    r = gen.rng(T + t_off)
+    qkv = gen.i8(r, (B, T, 3 * C))
+    tcap = (t_off + T + 15) // 16 * 16 + 16
+    dst0 = np.full((B, H, D, tcap), 0x55, np.int8)
+    src, dst = T_(qkv), T_(dst0)
+    iw._lib.call("iw_transpose_heads", src.data_ptr() + 2 * C, T * 3 * C, 3 * C, dst.data_ptr(), H * D * tcap,
+                 D * tcap, tcap, t_off, B, T, H, D, stream())
+    torch.cuda.synchronize()
+    exp = dst0.copy()
+    exp[:, :, :, t_off:t_off + T] = qkv[:, :, 2 * C:].reshape(B, T, H, D).transpose(0, 2, 3, 1)
+    assert np.array_equal(host(dst), exp)
 
 
 def test_embed_tokens(iw, oracle, gpu):
