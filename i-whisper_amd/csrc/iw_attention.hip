@@ -152,7 +152,8 @@ __device__ __forceinline__ int key_row(int kk) {
 }
 
 template <int KS, bool HAS_MASK>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3 : 1)))
+void attn_prefill_kernel(AttnArgs a) {
   constexpr int DP = KS * 32;           // padded head dim
   constexpr int KLD = DP + 16;          // sK row stride
   constexpr int VLD = PF_KC + 16;       // sVt row stride
@@ -192,16 +193,52 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
         qf[ks] = v4i{0, 0, 0, 0};
     }
 
-    auto stage_k = [&](int kc) {
-      constexpr int CPK = DP / 16;  // 16-byte chunks per key row
-      for (int c = tid; c < PF_KC * CPK; c += 256) {
+    // K and V^T chunks move global -> registers -> LDS. The next chunk's
+    // loads are issued as soon as the current one is in LDS, so their
+    // latency passes under the current chunk's MFMAs and softmax.
+    constexpr int CPK = DP / 16;                     // 16-byte chunks per key row
+    constexpr int KPT = (PF_KC * CPK + 255) / 256;   // K pieces per thread
+    constexpr int VPT = (DP * 4 + 255) / 256;        // V^T pieces per thread
+    uint4 kv[KPT], vv[VPT];
+    auto load_k = [&](int kc) {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int c = tid + 256 * j;
         const int kk = c / CPK, part = c % CPK;
         const int key = kc * PF_KC + kk;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (key < a.Tk && part * 16 < D)
-          val = *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * a.k_st + part * 16);
-        const int row = (kk & 32) + key_row(kk & 31);
-        *reinterpret_cast<uint4 *>(&sK[row * KLD + part * 16]) = val;
+        kv[j] = make_uint4(0, 0, 0, 0);
+        if (c < PF_KC * CPK && key < a.Tk && part * 16 < D)
+          kv[j] = *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * a.k_st + part * 16);
+      }
+    };
+    auto store_k = [&]() {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int c = tid + 256 * j;
+        if (c < PF_KC * CPK) {
+          const int kk = c / CPK, part = c % CPK;
+          const int row = (kk & 32) + key_row(kk & 31);
+          *reinterpret_cast<uint4 *>(&sK[row * KLD + part * 16]) = kv[j];
+        }
+      }
+    };
+    // V^T chunk: rows d, 64 keys each (4 pieces of 16 bytes)
+    auto load_v = [&](int kc) {
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = tid + 256 * j;
+        const int d = c >> 2, part = c & 3;
+        const int key0 = kc * PF_KC + part * 16;
+        vv[j] = make_uint4(0, 0, 0, 0);
+        if (c < DP * 4 && d < D && key0 < a.vt_ld)
+          vv[j] = *reinterpret_cast<const uint4 *>(vbase + (int64_t)d * a.vt_ld + key0);
+      }
+    };
+    auto store_v = [&]() {
+#pragma unroll
+      for (int j = 0; j < VPT; ++j) {
+        const int c = tid + 256 * j;
+        if (c < DP * 4) *reinterpret_cast<uint4 *>(&sVt[(c >> 2) * VLD + (c & 3) * 16]) = vv[j];
       }
     };
     auto scores = [&](int sub) {
@@ -218,9 +255,17 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
 
     // ---- pass 1: row max of the raw scores over unmasked keys ----
     int32_t mx = INT32_MIN;
+    load_k(0);
     for (int kc = 0; kc < nkc; ++kc) {
-      stage_k(kc);
+      store_k();
       __syncthreads();
+      // next: K chunk kc + 1, or pass 2's first K and V chunks
+      if (kc + 1 < nkc) {
+        load_k(kc + 1);
+      } else {
+        load_k(0);
+        load_v(0);
+      }
       // a chunk of keys all below Tk and no mask: no per-key test
       const bool full = !HAS_MASK && (kc + 1) * PF_KC <= a.Tk;
 #pragma unroll
@@ -259,17 +304,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
       for (int r = 0; r < 16; ++r) o[t][r] = 0;
     uint32_t psum = 0;
     for (int kc = 0; kc < nkc; ++kc) {
-      stage_k(kc);
-      // V^T chunk: rows d, 64 keys each (4 chunks of 16 bytes)
-      for (int c = tid; c < DP * 4; c += 256) {
-        const int d = c >> 2, part = c & 3;
-        const int key0 = kc * PF_KC + part * 16;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (d < D && key0 < a.vt_ld)
-          val = *reinterpret_cast<const uint4 *>(vbase + (int64_t)d * a.vt_ld + key0);
-        *reinterpret_cast<uint4 *>(&sVt[d * VLD + part * 16]) = val;
-      }
+      store_k();
+      store_v();
       __syncthreads();
+      if (kc + 1 < nkc) {
+        load_k(kc + 1);
+        load_v(kc + 1);
+      }
       const bool full = !HAS_MASK && (kc + 1) * PF_KC <= a.Tk;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
