@@ -64,11 +64,12 @@ SIGNATURES = {
     "iw_frag_pack": [_p, _i64, _i64, _i64, _p, _p],
     "iw_linear8_frag": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _b, _b, _b, _p],
     "iw_linear8_gelu_frag": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64,
-                             _i64, _b, _b, _b, _p],
+                             _i64, _b, _b, _b, _p, _i64, _i64, _p],
     "iw_linear32_residual15_frag": [_p, _p, _p, _p, _p, _p, _p, _u16, _p, _i64, _i64, _i64, _b, _b, _p],
     "iw_linear8_qkv_cache_frag": [_p, _p, _p, _p, _p, _p, _i64, _i64, _b, _b, _p, _i64, _p, _i64, _i64,
                                   _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
-    "iw_layernorm32_frag": [_p, _p, _p, _u8, _i8, _u32, _i8, _u32, _p, _i64, _i64, _b, _p],
+    "iw_layernorm32_frag": [_p, _p, _p, _u8, _i8, _u32, _i8, _u32, _p, _i64, _i64, _b, _p, _i64, _i64,
+                            _p],
     "iw_attention_decode_cache_frag": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
                                        _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32, _p],
     "iw_classifier_frag": [_p, _p, _u32, _i8, _p, _i64, _i64, _i64, _p],

@@ -114,7 +114,7 @@ int qkv_cache_args(const int8_t *x, const int8_t *weight, const int32_t *bias, c
 int layernorm32_entry(const int16_t *x, const int8_t *weight, const int32_t *bias, uint8_t ln_multiplier,
                       int8_t ln_shift, uint32_t out_multiplier, int8_t out_shift, uint32_t rsqrt_offset,
                       int8_t *out, int64_t rows, int64_t hidden, bool has_bias, bool out_frag,
-                      iw_stream_t stream) {
+                      iw_stream_t stream, const FragPrefetch *pf = nullptr) {
   IW_REQUIRE(layernorm_width_code(hidden) >= 0,
              "unsupported LayerNorm hidden size: " + std::to_string(hidden));
   IW_REQUIRE(rows >= 0, "invalid row count");
@@ -125,7 +125,7 @@ int layernorm32_entry(const int16_t *x, const int8_t *weight, const int32_t *bia
              "LayerNorm input must be 8-byte and output 4-byte aligned");
   return launch_layernorm32(x, weight, has_bias ? bias : nullptr, ln_multiplier, ln_shift,
                             out_multiplier, out_shift, rsqrt_offset, out, rows, hidden,
-                            as_stream(stream), out_frag);
+                            as_stream(stream), out_frag, pf);
 }
 
 int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb, int64_t k_sh,
@@ -192,6 +192,20 @@ int check_frag(const void *x, const void *w, int64_t M, int64_t K, int64_t N) {
   IW_REQUIRE(N <= 0x7fffff00LL, "N too large");
   IW_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15) == 0,
              "fragment-major operands must be 16-byte aligned");
+  return IW_OK;
+}
+
+// The fragment-major weight [next_n][next_k] of the decode GEMM that runs
+// next, as a prefetch hint; none when next_weight is null.
+int frag_prefetch_args(const int8_t *next_weight, int64_t next_n, int64_t next_k, FragPrefetch *pf) {
+  *pf = FragPrefetch();
+  if (!next_weight) return IW_OK;
+  IW_REQUIRE(next_n > 0 && next_k > 0 && next_k <= kFragMaxK && frag_rpad(next_n) * frag_kpad(next_k) < (1LL << 31),
+             "invalid prefetch weight shape");
+  IW_REQUIRE((reinterpret_cast<uintptr_t>(next_weight) & 15) == 0, "prefetch weight must be 16-byte aligned");
+  pf->w = next_weight;
+  pf->tile_bytes = 32 * frag_kpad(next_k);
+  pf->tiles = (int)((next_n + 31) / 32);
   return IW_OK;
 }
 
@@ -774,12 +788,15 @@ int iw_linear8_gelu_frag(const int8_t *x, const int8_t *weight, const int32_t *b
                          const uint8_t *luti_multiplier, const int8_t *luti_shift, const uint8_t *luto_multiplier,
                          const int8_t *luto_shift, int64_t luti_count, int64_t luto_count, int8_t *out, int64_t M,
                          int64_t K, int64_t N, bool has_bias, bool asymmetric, bool out_frag,
-                         iw_stream_t stream) {
+                         const int8_t *next_weight, int64_t next_n, int64_t next_k, iw_stream_t stream) {
   int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, out, M, K, N, has_bias, asymmetric);
   if (rc) return rc;
   rc = check_gelu_counts(N, luti_count, luto_count);
   if (rc || M == 0) return rc;
   rc = check_frag(x, weight, M, K, N);
+  if (rc) return rc;
+  FragPrefetch pf;
+  rc = frag_prefetch_args(next_weight, next_n, next_k, &pf);
   if (rc) return rc;
   IW_REQUIRE(!out_frag || N <= kFragMaxK, "a fragment-major output has at most 5120 columns");
   IW_REQUIRE(lut && luti_multiplier && luti_shift && luto_multiplier && luto_shift, "null GeLU parameter pointer");
@@ -792,6 +809,7 @@ int iw_linear8_gelu_frag(const int8_t *x, const int8_t *weight, const int32_t *b
   g.luto_s = luto_shift;
   g.luti_pc = luti_count != 1;
   g.luto_pc = luto_count != 1;
+  g.pf = pf;
   if (out_frag) g.ldc = frag_kpad(N);
   return gemm_frag(g, nullptr, out_frag, as_stream(stream));
 }
@@ -833,9 +851,13 @@ int iw_linear8_qkv_cache_frag(const int8_t *x, const int8_t *weight, const int32
 
 int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *bias, uint8_t ln_multiplier,
                         int8_t ln_shift, uint32_t out_multiplier, int8_t out_shift, uint32_t rsqrt_offset,
-                        int8_t *out, int64_t rows, int64_t hidden, bool has_bias, iw_stream_t stream) {
+                        int8_t *out, int64_t rows, int64_t hidden, bool has_bias, const int8_t *next_weight,
+                        int64_t next_n, int64_t next_k, iw_stream_t stream) {
+  FragPrefetch pf;
+  const int rc = frag_prefetch_args(next_weight, next_n, next_k, &pf);
+  if (rc) return rc;
   return layernorm32_entry(x, weight, bias, ln_multiplier, ln_shift, out_multiplier, out_shift, rsqrt_offset, out,
-                           rows, hidden, has_bias, true, stream);
+                           rows, hidden, has_bias, true, stream, &pf);
 }
 
 int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb, int64_t k_sh,

@@ -17,6 +17,22 @@ enum GemmEpi : int {
 
 enum GemmOut : int { OUT_ROW = 0, OUT_NCT = 1 };
 
+// The fragment-major weight of the decode GEMM that runs after the current
+// kernel (layout: frag_offset below). Its column tile t is the tile_bytes =
+// 32 * Kp contiguous bytes at w + t * tile_bytes, and gemm_frag_kernel reads
+// it only on the XCD of blockIdx t % 8 (blocks are dealt round-robin over
+// the 8 XCDs). A kernel given one reads, on each XCD, the tiles that XCD's
+// GEMM blocks will read, so that they come from its L2 rather than HBM.
+// A hint: no result depends on it.
+struct FragPrefetch {
+  const int8_t *w = nullptr;
+  int64_t tile_bytes = 0;
+  int tiles = 0;
+  // the launch that reads them: its grid and block sizes
+  // (frag_prefetch_launch fills them in)
+  int blocks = 0, threads = 0;
+};
+
 struct GemmArgs {
   // A operand
   const int8_t *a = nullptr;
@@ -57,6 +73,8 @@ struct GemmArgs {
   void *out = nullptr;
   int64_t ldc = 0;
   int64_t out_T = 1;  // OUT_NCT: rows are (b, t) with t in [0, out_T)
+  // the next decode GEMM's weight, read into L2 (gemm_frag_kernel only)
+  FragPrefetch pf;
 };
 
 // Decode-step QKV projection: the epilogue writes Q (columns [0, C)) to
@@ -93,6 +111,57 @@ __host__ __device__ inline int64_t frag_kpad(int64_t k) { return (k + 319) / 320
 __host__ __device__ inline int64_t frag_rpad(int64_t r) { return (r + 31) / 32 * 32; }
 __host__ __device__ inline int64_t frag_offset(int64_t r, int64_t k, int64_t kp) {
   return (r >> 5) * 32 * kp + (k >> 5) * 1024 + ((r & 31) + ((k >> 4) & 1) * 32) * 16 + (k & 15);
+}
+
+// Fills in the launch geometry of a prefetch (grid and block size).
+inline void frag_prefetch_launch(FragPrefetch &p, int64_t blocks, int threads) {
+  p.blocks = (int)blocks;
+  p.threads = threads;
+}
+
+// NL dword loads per thread, one per 64 bytes of the column tiles that the
+// next GEMM reads on this block's XCD (XCD blockIdx % 8), spread over this
+// launch's blocks on that XCD; lines beyond NL per thread are left to HBM.
+// The loads are unconditional, so that the compiler counts them and its
+// waits for the kernel's own (earlier) loads leave them in flight: a lane
+// with no line to fetch, or a launch with no hint, reads `fallback` (an
+// address the kernel reads anyway). Pass v to frag_prefetch_keep at the end.
+// The launch geometry comes from p (kernel arguments), not from the
+// dispatch packet, whose read would be a vector-memory wait of its own.
+template <int NL>
+__device__ inline void frag_prefetch_issue(const FragPrefetch &p, const void *fallback, uint32_t (&v)[NL]) {
+  const int blk = (int)blockIdx.x, xcd = blk & 7;
+  const bool on = p.w != nullptr && p.tiles > xcd;
+  const uint32_t per = ((uint32_t)p.blocks - (uint32_t)xcd + 7) >> 3;      // this launch's blocks on the XCD
+  const uint32_t ntx = on ? ((uint32_t)p.tiles - (uint32_t)xcd + 7) >> 3 : 0;  // the next GEMM's tiles on it
+  const uint32_t tb = (uint32_t)p.tile_bytes;                              // < 2^31 (host-checked)
+  const uint32_t lpt = max(tb >> 6, 1u);                                     // 64-byte lines per tile
+  const uint32_t step = per * (uint32_t)p.threads;
+  const uint32_t u0 = (uint32_t)(blk >> 3) * (uint32_t)p.threads + threadIdx.x;
+  // line u of the XCD's tiles = (tile t, line c): walked by `step` per load
+  uint32_t t = u0 / lpt, c = u0 - t * lpt;
+  const uint32_t dq = step / lpt, dr = step - dq * lpt;
+  // 32-bit offsets (the whole weight is < 2^31 bytes) and selects, so that
+  // no branch or 64-bit multiply sits between the loads
+  const int8_t *base = on ? p.w + (uint32_t)xcd * tb : reinterpret_cast<const int8_t *>(fallback);
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const bool in = t < ntx;
+    const uint32_t off = in ? 8 * t * tb + c * 64 : 0u;
+    const int8_t *a = in ? base : reinterpret_cast<const int8_t *>(fallback);
+    v[i] = *reinterpret_cast<const uint32_t *>(a + off);
+    c += dr;
+    t += dq;
+    if (c >= lpt) c -= lpt, ++t;
+  }
+}
+
+template <int NL>
+__device__ inline void frag_prefetch_keep(const uint32_t (&v)[NL]) {
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) x ^= v[i];
+  asm volatile("" ::"v"(x));
 }
 
 // a and b fragment-major with padded K = frag_kpad(K); out_frag: the int8

@@ -79,6 +79,19 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
     fa[t] = *reinterpret_cast<const v4i *>(pa + t * 1024);
     fb[t] = *reinterpret_cast<const v4i *>(pb + t * 1024);
   }
+  // FC1 (the GeLU instances) reads FC2's weight tiles into L2 behind its own
+  // operands, when given them: 1 line per thread covers 2.5 MB per XCD with
+  // 128 rows of Whisper-large (FC2's weight share is 0.8 MB). The GEMMs
+  // before an attention kernel take no hint: the K/V stream evicts the lines
+  // before the GEMM after it runs.
+  constexpr bool PF = GELU;
+  uint32_t pfv[1];
+  if constexpr (PF) {
+    frag_prefetch_issue(g.pf, pb, pfv);
+    // issued here, with the operands, not sunk below the MFMAs: the wait
+    // after the partial-tile barrier below covers every load
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   // two accumulator chains so that consecutive MFMAs do not wait on each
   // other; row sums of A for the zero-point term from the same registers
@@ -105,7 +118,10 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
   __syncthreads();
 
-  if (n >= N) return;
+  if (n >= N) {
+    if constexpr (PF) frag_prefetch_keep(pfv);
+    return;
+  }
   const bool zp = g.wz != nullptr;
   const ColParams c = decode_col<EPI>(g, craw);
 #pragma unroll
@@ -124,6 +140,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
                                                  EPI == EPI_L32RES ? resv[j] : 0);
     }
   }
+  if constexpr (PF) frag_prefetch_keep(pfv);
 }
 
 template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, int SPW, int MAXW, int MINW>
@@ -132,7 +149,9 @@ int launch_frag_waves(const GemmArgs &g, const SkinnyScatter &sc, int64_t kp, hi
   const int ms = (int)((g.M + 31) / 32);
   const int nw = (int)(kp / (32 * SPW));
   const dim3 grid((unsigned)(((tiles + 7) / 8) * 8 * ms));
-  hipLaunchKernelGGL((gemm_frag_kernel<EPI, GELU, SCATTER, OUT_FRAG, SPW, MAXW, MINW>), grid, dim3(64 * nw), 0, s, g,
+  GemmArgs ga = g;
+  frag_prefetch_launch(ga.pf, grid.x, 64 * nw);
+  hipLaunchKernelGGL((gemm_frag_kernel<EPI, GELU, SCATTER, OUT_FRAG, SPW, MAXW, MINW>), grid, dim3(64 * nw), 0, s, ga,
                      sc, ms, (int)tiles, (int)kp);
   return check_launch("gemm_frag_kernel");
 }

@@ -9,6 +9,8 @@
 
 namespace iw {
 
+struct FragPrefetch;  // iw_gemm.hpp
+
 // Fused attention arguments. Element (b, t, h, d) of a [B, T, H*D] operand
 // lives at base + b * sb + t * st + h * D + d. V is given transposed per
 // head: vt + b * v_sb + h * v_sh + d * v_sd + t (prefill: v_sh = D * vt_ld,
@@ -39,7 +41,8 @@ int layernorm_width_code(int64_t h);
 // out_frag: out is the fragment-major image of [rows][hidden] (rows <= 128)
 int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
                        int8_t ln_s, uint32_t out_m, int8_t out_s, uint32_t rsqrt_off, int8_t *out,
-                       int64_t rows, int64_t hidden, hipStream_t s, bool out_frag = false);
+                       int64_t rows, int64_t hidden, hipStream_t s, bool out_frag = false,
+                       const FragPrefetch *pf = nullptr);
 int launch_rsqrt(const int32_t *x, int32_t *out, int64_t n, uint32_t off, hipStream_t s);
 int launch_gelu(const int8_t *x, const uint8_t *lut, const uint8_t *luti_m, const int8_t *luti_s,
                 const uint8_t *luto_m, const int8_t *luto_s, int8_t *out, int64_t numel,

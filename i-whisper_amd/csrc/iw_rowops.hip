@@ -236,13 +236,15 @@ __global__ __launch_bounds__(256) void layernorm32_kernel(
 
 // LayerNorm32 for few rows (a decode step): one row per block of 256 threads,
 // thread t owning elements t, t + 256, ... so that each row's arithmetic is
-// spread over four SIMDs. Same integer steps as layernorm32_kernel.
+// spread over four SIMDs. Same integer steps as layernorm32_kernel. With
+// pf.w set, the blocks also read the next decode GEMM's weight tiles into
+// their XCDs' L2 (behind the row's own loads).
 constexpr int LNR_MAX = 5;  // 1280 / 256
 __global__ __launch_bounds__(256) void layernorm32_row_kernel(
     const int16_t *__restrict__ x, const int8_t *__restrict__ gamma,
     const int32_t *__restrict__ beta, uint32_t ln_m, int32_t ln_s, uint32_t out_m,
     int32_t out_s, uint32_t rsqrt_off, int8_t *__restrict__ out, int hidden, int code,
-    int64_t out_frag_kp) {
+    int64_t out_frag_kp, FragPrefetch pf) {
   __shared__ uint32_t sA[4], sB[4], sC[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
@@ -256,8 +258,13 @@ __global__ __launch_bounds__(256) void layernorm32_row_kernel(
     v[j] = ok ? xr[e] : 0;
     gm[j] = ok ? gamma[e] : 0;
     bt[j] = (ok && beta) ? beta[e] : 0;
-    sum += (uint32_t)v[j];
   }
+  // 4 lines per thread: 1 MB per XCD at 128 rows, more than any decode
+  // GEMM's weight share (FC1's is 0.8 MB at Whisper-large)
+  uint32_t pfv[4];
+  frag_prefetch_issue(pf, xr, pfv);
+#pragma unroll
+  for (int j = 0; j < LNR_MAX; ++j) sum += (uint32_t)v[j];
   sum = wave_sum_dpp(sum);
   if (lane == 0) sA[wave] = sum;
   __syncthreads();
@@ -308,6 +315,7 @@ __global__ __launch_bounds__(256) void layernorm32_row_kernel(
         orow[e] = yo;
     }
   }
+  frag_prefetch_keep(pfv);
 }
 
 __global__ void rsqrt_kernel(const int32_t *x, int32_t *out, int64_t n, uint32_t off) {
@@ -857,16 +865,18 @@ int layernorm_width_code(int64_t h) {
 
 int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
                        int8_t ln_s, uint32_t out_m, int8_t out_s, uint32_t rsqrt_off, int8_t *out,
-                       int64_t rows, int64_t hidden, hipStream_t s, bool out_frag) {
+                       int64_t rows, int64_t hidden, hipStream_t s, bool out_frag, const FragPrefetch *pf) {
   const int code = layernorm_width_code(hidden);
   if (code < 0) return fail("unsupported LayerNorm hidden size: " + std::to_string(hidden));
   if (rows == 0) return 0;
   if (out_frag && rows > kSkinnyMaxRows) return fail("a fragment-major LayerNorm output takes at most 128 rows");
   if (rows <= kLnRowBlockMaxRows) {
     // few rows (a decode step): a block of 256 threads per row
+    FragPrefetch pfl = pf ? *pf : FragPrefetch();
+    frag_prefetch_launch(pfl, rows, 256);
     hipLaunchKernelGGL(layernorm32_row_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, gamma, beta,
                        (uint32_t)ln_m, (int32_t)ln_s, out_m, (int32_t)out_s, rsqrt_off, out, (int)hidden,
-                       code, out_frag ? frag_kpad(hidden) : (int64_t)0);
+                       code, out_frag ? frag_kpad(hidden) : (int64_t)0, pfl);
     return check_launch("layernorm32_row_kernel");
   }
   // one row per wave at a time, four waves per block; persistent waves, as

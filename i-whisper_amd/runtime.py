@@ -108,11 +108,21 @@ def _frag_buffer(rows: int, cols: int, dev) -> torch.Tensor:
     return torch.zeros(_lib.value("iw_frag_bytes", rows, cols), dtype=torch.int8, device=dev)
 
 
-def _ln_frag(ln, x: torch.Tensor, rows: int, out: torch.Tensor):
+_NO_PREFETCH = (None, 0, 0)
+
+
+def _pf_args(nxt: Optional["_FragLinear"]):
+    """The prefetch-hint arguments naming ``nxt``'s weight (or none)."""
+    return nxt.pf() if nxt is not None else _NO_PREFETCH
+
+
+def _ln_frag(ln, x: torch.Tensor, rows: int, out: torch.Tensor, nxt: Optional["_FragLinear"] = None):
+    """LayerNorm into a fragment-major operand; ``nxt``: the GEMM that reads it,
+    whose weight tiles the launch reads into L2 on the way."""
     s = ln._scalars()
     _lib.call("iw_layernorm32_frag", x.data_ptr(), ln.weight.data_ptr(), _ptr(ln.bias), s["lm"],
               s["ls"], s["om"], s["os"], ln.offset, out.data_ptr(), rows, ln.normalized_shape[0],
-              ln.bias is not None, _stream())
+              ln.bias is not None, *_pf_args(nxt), _stream())
     return out
 
 
@@ -133,6 +143,10 @@ class _FragLinear:
     def args(self):
         return (self.w.data_ptr(), _ptr(self.bias), _ptr(self.wz), self.mult.data_ptr(),
                 self.shift.data_ptr())
+
+    def pf(self):
+        """The prefetch-hint arguments naming this GEMM's weight."""
+        return (self.w.data_ptr(), self.N, self.K)
 
     def linear8(self, xf: torch.Tensor, M: int, out: torch.Tensor, out_frag: bool = False):
         _lib.call("iw_linear8_frag", xf.data_ptr(), *self.args(), out.data_ptr(), M, self.K, self.N,
@@ -263,7 +277,7 @@ class DecoderRunner:
 
     def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int,
                  max_steps: Optional[int] = None, use_graph: bool = True,
-                 filters: Optional[LogitFilters] = None, frag: bool = True):
+                 filters: Optional[LogitFilters] = None, frag: bool = True, prefetch: bool = True):
         self.dec = decoder
         self.B = batch
         C, H = decoder.n_state, decoder.n_head
@@ -294,6 +308,9 @@ class DecoderRunner:
         self.logits = torch.empty((batch, decoder.n_vocab), **i8)
         # fragment-major weights and activations of the one-token step
         self.frag = frag and batch <= 128 and 4 * C <= 5120
+        # each LayerNorm (and FC1) of the one-token step reads the next
+        # GEMM's weight tiles into L2 (a hint; results do not depend on it)
+        self.prefetch = prefetch
         if self.frag:
             self.f_qkv = [_FragLinear(f) for f in self.self_qkv]
             self.f_out = [_FragLinear(b.attn.out) for b in decoder.blocks]
@@ -486,10 +503,11 @@ class DecoderRunner:
         dec = self.dec
         B, C, H, D = self.B, self.C, self.H, self.D
         x16, q8, h8f, wvf, f8f = self.x16, self.q8, self.h8f, self.wvf, self.f8f
+        pf = (lambda f: f) if self.prefetch else (lambda f: None)
         for l, blk in enumerate(dec.blocks):
             sc = blk._scalars()
             fq = self.f_qkv[l]
-            _ln_frag(blk.attn_ln, x16, B, h8f)
+            _ln_frag(blk.attn_ln, x16, B, h8f, pf(fq))
             _lib.call("iw_linear8_qkv_cache_frag", h8f.data_ptr(), *fq.args(), B, C, True, True,
                       q8.data_ptr(), C, self.k_self[l].data_ptr(), H * self.Tcap * D, self.Tcap * D, D,
                       self.vt_self[l].data_ptr(), H * D * self.tcap16, D * self.tcap16, self.tcap16, C,
@@ -501,7 +519,7 @@ class DecoderRunner:
                       self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
                       blk.attn.rsqrt_offset, _stream())
             self.f_out[l].linear32_res(wvf, B, x16, sc["a"])
-            _ln_frag(blk.cross_attn_ln, x16, B, h8f)
+            _ln_frag(blk.cross_attn_ln, x16, B, h8f, pf(self.f_cq[l]))
             self.f_cq[l].linear8(h8f, B, q8)
             s = blk.cross_attn._scalars()
             Ta = self.Ta
@@ -510,14 +528,14 @@ class DecoderRunner:
                       D * self.ta16, self.ta16, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
                       s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
             self.f_co[l].linear32_res(wvf, B, x16, sc["c"])
-            _ln_frag(blk.mlp_ln, x16, B, h8f)
-            fc1, gelu = blk.mlp[0], blk.mlp[1]
-            lut, im, is_, om, os_, ci, co = gelu.gelu_ptrs()
-            f1 = self.f_fc1[l]
+            f1, f2 = self.f_fc1[l], self.f_fc2[l]
+            _ln_frag(blk.mlp_ln, x16, B, h8f, pf(f1))
+            lut, im, is_, om, os_, ci, co = blk.mlp[1].gelu_ptrs()
+            nxt = pf(f2)
             _lib.call("iw_linear8_gelu_frag", h8f.data_ptr(), *f1.args(), lut, im, is_, om, os_, ci, co,
                       f8f.data_ptr(), B, f1.K, f1.N, f1.bias is not None, f1.wz is not None, True,
-                      _stream())
-            self.f_fc2[l].linear32_res(f8f, B, x16, sc["m"])
+                      *_pf_args(nxt), _stream())
+            f2.linear32_res(f8f, B, x16, sc["m"])
 
     def _replay(self, n: int):
         if n <= 0:

@@ -342,7 +342,10 @@ int iw_frag_pack(const int8_t *src, int64_t rows, int64_t cols, int64_t ld, int8
 
 /* iw_linear8 / iw_linear8_gelu with x and weight fragment-major (M <= 128);
  * out is row-major [M][N] or, when out_frag, the fragment-major image of
- * [M][N]. */
+ * [M][N]. iw_linear8_gelu_frag's next_weight (optional, NULL for none): the
+ * fragment-major weight [next_n][next_k] of the decode GEMM that runs next;
+ * the launch also reads its column tiles into the L2 of the XCD that GEMM
+ * reads each tile on. A prefetch hint: the results do not depend on it. */
 int iw_linear8_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
                     const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
                     int8_t *out, int64_t M, int64_t K, int64_t N, bool has_bias, bool asymmetric,
@@ -352,7 +355,8 @@ int iw_linear8_gelu_frag(const int8_t *x, const int8_t *weight, const int32_t *b
                          const uint8_t *lut, const uint8_t *luti_multiplier, const int8_t *luti_shift,
                          const uint8_t *luto_multiplier, const int8_t *luto_shift, int64_t luti_count,
                          int64_t luto_count, int8_t *out, int64_t M, int64_t K, int64_t N,
-                         bool has_bias, bool asymmetric, bool out_frag, iw_stream_t stream);
+                         bool has_bias, bool asymmetric, bool out_frag, const int8_t *next_weight,
+                         int64_t next_n, int64_t next_k, iw_stream_t stream);
 
 /* iw_linear32_residual15 with x and weight fragment-major (M <= 128). */
 int iw_linear32_residual15_frag(const int8_t *x, const int8_t *weight, const int32_t *bias,
@@ -372,11 +376,13 @@ int iw_linear8_qkv_cache_frag(const int8_t *x, const int8_t *weight, const int32
                               int64_t cache_positions, const int32_t *pos, iw_stream_t stream);
 
 /* iw_layernorm32 writing the fragment-major image of out [rows][hidden]
- * (rows <= 128). */
+ * (rows <= 128); next_weight / next_n / next_k: the prefetch hint of
+ * iw_linear8_gelu_frag (the GEMM that reads out). */
 int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *bias,
                         uint8_t ln_multiplier, int8_t ln_shift, uint32_t out_multiplier,
                         int8_t out_shift, uint32_t rsqrt_offset, int8_t *out, int64_t rows,
-                        int64_t hidden, bool has_bias, iw_stream_t stream);
+                        int64_t hidden, bool has_bias, const int8_t *next_weight, int64_t next_n,
+                        int64_t next_k, iw_stream_t stream);
 
 /* iw_attention_decode_cache writing the fragment-major image of out
  * [batch][heads*head_dim] (batch <= 128, heads*head_dim <= 5120). */

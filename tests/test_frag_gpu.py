@@ -105,11 +105,17 @@ def test_linear8_gelu_frag(iw, oracle, gpu, M, K, N):
     exp = oracle.gelu(oracle.linear8(x, w, b, z, m, s), lut, im, is_, om, os_)
     xf, wf = pack(iw, x), pack(iw, w)
     ts = [T(a) for a in (b, z, m, s, lut, im, is_, om, os_)]
-    of = zeros_frag(iw, M, N)
-    iw._lib.call("iw_linear8_gelu_frag", xf.data_ptr(), wf.data_ptr(), *[t.data_ptr() for t in ts], N, N,
-                 of.data_ptr(), M, K, N, True, True, True, stream())
-    torch.cuda.synchronize()
-    assert np.array_equal(host(of), frag_image(exp))
+    # without and with the prefetch hint (the next GEMM's weight, N2 x K2):
+    # the same output
+    r = gen.rng(M + 2 * N)
+    n2, k2 = (1280, 5120) if K == 1280 else (33, 700)
+    nxt = pack(iw, gen.i8(r, (n2, k2)))
+    for pf in ((None, 0, 0), (nxt.data_ptr(), n2, k2)):
+        of = zeros_frag(iw, M, N)
+        iw._lib.call("iw_linear8_gelu_frag", xf.data_ptr(), wf.data_ptr(), *[t.data_ptr() for t in ts], N, N,
+                     of.data_ptr(), M, K, N, True, True, True, *pf, stream())
+        torch.cuda.synchronize()
+        assert np.array_equal(host(of), frag_image(exp)), pf[1:]
 
 
 @pytest.mark.parametrize("M,K,N", [(128, 1280, 1280), (128, 5120, 1280), (37, 1536, 384), (1, 2560, 64),
@@ -151,11 +157,15 @@ def test_layernorm32_frag(iw, oracle, gpu, hidden, rows):
     x, g, b, lm, ls, om, os_ = gen.ln_case(hidden * 3 + rows, rows, hidden, 4000)
     exp = oracle.layernorm32(x, g, b, lm, ls, om, os_)
     xt, gt, bt = T(x), T(g), T(b)
-    of = zeros_frag(iw, rows, hidden)
-    iw._lib.call("iw_layernorm32_frag", xt.data_ptr(), gt.data_ptr(), bt.data_ptr(), lm, ls, om, os_, 13,
-                 of.data_ptr(), rows, hidden, True, stream())
-    torch.cuda.synchronize()
-    assert np.array_equal(host(of), frag_image(exp))
+    # without and with the prefetch hint (a QKV-shaped next weight, and one
+    # with fewer column tiles than XCDs): the same output
+    nxt = pack(iw, gen.i8(gen.rng(rows + hidden), (3 * hidden, hidden)))
+    for pf in ((None, 0, 0), (nxt.data_ptr(), 3 * hidden, hidden), (nxt.data_ptr(), 70, hidden)):
+        of = zeros_frag(iw, rows, hidden)
+        iw._lib.call("iw_layernorm32_frag", xt.data_ptr(), gt.data_ptr(), bt.data_ptr(), lm, ls, om, os_, 13,
+                     of.data_ptr(), rows, hidden, True, *pf, stream())
+        torch.cuda.synchronize()
+        assert np.array_equal(host(of), frag_image(exp)), pf[1:]
 
 
 def test_layernorm32_frag_rejects_many_rows(iw, gpu):
@@ -164,7 +174,20 @@ def test_layernorm32_frag_rejects_many_rows(iw, gpu):
     of = zeros_frag(iw, 129, 384)
     with pytest.raises(RuntimeError, match="at most 128 rows"):
         iw._lib.call("iw_layernorm32_frag", x.data_ptr(), g.data_ptr(), None, 1, 1, 1, 1, 13, of.data_ptr(),
-                     129, 384, False, stream())
+                     129, 384, False, None, 0, 0, stream())
+
+
+def test_frag_prefetch_hint_is_checked(iw, gpu):
+    x = torch.zeros((4, 384), dtype=torch.int16, device="cuda")
+    g = torch.zeros(384, dtype=torch.int8, device="cuda")
+    of = zeros_frag(iw, 4, 384)
+    w = zeros_frag(iw, 64, 384)
+    for n, k, what in ((64, 6000, "prefetch weight shape"), (0, 384, "prefetch weight shape"),
+                       (64, 384, "16-byte aligned")):
+        ptr = w.data_ptr() + (4 if what == "16-byte aligned" else 0)
+        with pytest.raises(RuntimeError, match=what):
+            iw._lib.call("iw_layernorm32_frag", x.data_ptr(), g.data_ptr(), None, 1, 1, 1, 1, 13,
+                         of.data_ptr(), 4, 384, False, ptr, n, k, stream())
 
 
 @pytest.mark.parametrize("B,H,D,Tk,tcap,k_length", [(2, 3, 64, 17, 448, 1), (128, 20, 64, 1500, 1500, 1500),
