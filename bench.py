@@ -96,8 +96,8 @@ PMC_SUMMARIES = (ROOT / "profiles" / "attn_decode_cross_b128_pmc.md",
                  ROOT / "profiles" / "encoder_gemm_large_b128_pmc.md")
 GEMM_TRAFFIC_KEY = "gemm_dtl_kernel (encoder layer average)"
 # the decoder cross-attention kernel as profilers name it (key capacity, ring
-# slots, keys per chunk)
-XA_KERNEL = "attn_decode_stream_kernel<2048, 3, 128>"
+# slots, keys per chunk, waves per (batch, head))
+XA_KERNEL = "attn_decode_stream_kernel<2048, 3, 128, 4>"
 
 
 def recorded_traffic(kernel: str):

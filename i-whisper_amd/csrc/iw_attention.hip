@@ -699,7 +699,8 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 // bytes in flight (bandwidth x latency). Both operands flow through one ring
 // of NR slots in CH-key chunks: K chunks 0 .. nK-1, then V^T chunks, so the
 // copies of V are already under way while the row maximum and P are formed.
-// A chunk is DPC = CH / 64 global_load_lds_dwordx4 copies per wave, and every
+// A chunk is DPC = CH / (16 NW) global_load_lds_dwordx4 copies for each of
+// the block's NW waves (K: 16 keys per copy; V^T: 64 / NW rows), and every
 // lane later reads back exactly the 16-byte pieces it copied (K: one key's
 // 16 (l % 4)-th piece; V^T: one d-row's piece of 16 keys), so a wave only
 // waits for its own copies (vmcnt) and the ring needs no barrier. Keys past
@@ -756,20 +757,30 @@ __device__ __forceinline__ void lds_barrier() {
 #ifndef IW_DSS_CH
 #define IW_DSS_CH 128
 #endif
+// waves per (batch, head) of the self-attention instance. Two waves with
+// 64-key chunks (13.8 KB of LDS) make the 2560 heads of a batch of 128
+// resident at once instead of in two rounds, and are faster on one layer's
+// cache replayed (partly Infinity-Cache-resident), but slower inside the
+// decode step, where every layer's cache streams from HBM (22.4 against
+// 21.4 us per launch).
+#ifndef IW_DSS_NW
+#define IW_DSS_NW 4
+#endif
 
-template <int MAXK, int NR, int CH>
-__global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
+template <int MAXK, int NR, int CH, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
   constexpr int D = 64;
-  constexpr int DPC = CH / 64;        // copies per wave per chunk
-  constexpr int SLOT = 4096 * DPC;    // bytes per ring slot
+  constexpr int DPC = CH / (16 * NW);  // copies per wave per chunk
+  constexpr int SLOT = 1024 * NW * DPC;  // bytes per ring slot (CH keys x 64 bytes)
+  static_assert(DPC >= 1 && 16 * NW * DPC == CH, "a chunk is whole 1 KB copies of every wave");
   constexpr int WB = 1024 * DPC;      // bytes per wave per slot
-  constexpr int LPR = 4 * DPC;        // lanes per V^T row piece set
+  constexpr int LPR = CH / 16;        // lanes per V^T row piece set
   constexpr int RPD = 64 / LPR;       // V^T rows per copy
   __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
   __shared__ int16_t sS[MAXK];  // requantized scores
   __shared__ __attribute__((aligned(16))) uint8_t sP[MAXK];
-  __shared__ int32_t sRed[4];
-  __shared__ uint32_t sSum[4];
+  __shared__ int32_t sRed[NW];
+  __shared__ uint32_t sSum[NW];
   __shared__ uint32_t sHi;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -788,7 +799,7 @@ __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, con
   const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh + cq * 16;
   // V^T: copy u brings row wave*16 + u*RPD + l/LPR, keys 16 (l % LPR) .. +16
   const int vp = lane % LPR;
-  const int vrow = wave * 16 + lane / LPR;
+  const int vrow = wave * (64 / NW) + lane / LPR;
   const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)vrow * a.v_sd;
   const int vlast = Tk > 0 ? ((Tk - 1) & ~15) : 0;  // last V^T piece holding a valid key
   const uint32_t ring =
@@ -833,10 +844,12 @@ __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, con
     for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
     if (lane == 0) sRed[wave] = mx;
     lds_barrier();
-    const int32_t rowmax = max(max(sRed[0], sRed[1]), max(sRed[2], sRed[3]));
+    int32_t rowmax = sRed[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) rowmax = max(rowmax, sRed[w]);
     const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
     uint32_t psum = 0, hi = 0;
-    for (int j = tid; j < nK * CH; j += 256) {
+    for (int j = tid; j < nK * CH; j += 64 * NW) {
       uint32_t p = 0;
       // x_sub = qk - rmp1 modulo 2^16
       if (j < Tk) p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)sS[j] - rmp1), a.frac_bits);
@@ -849,7 +862,10 @@ __global__ __launch_bounds__(256) void attn_decode_stream_kernel(AttnArgs a, con
     if (lane == 0) sSum[wave] = psum;
     if (hi & 0x80u) atomicOr(&sHi, 1u);
     lds_barrier();
-    inv = fisr((int32_t)(sSum[0] + sSum[1] + sSum[2] + sSum[3]), a.rsqrt_off);
+    uint32_t total = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) total += sSum[w];
+    inv = fisr((int32_t)total, a.rsqrt_off);
     any_hi = sHi != 0;
   };
 
@@ -996,7 +1012,8 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
     // (self-attention caches up to 512 positions get their own, smaller
     // instance, so profiles separate it from cross-attention)
     if (a.max_tk <= 512)
-      hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DSS_NR, IW_DSS_CH>), grid, dim3(256), 0, s, a, pos);
+      hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DSS_NR, IW_DSS_CH, IW_DSS_NW>), grid, dim3(64 * IW_DSS_NW),
+                         0, s, a, pos);
     else if (a.max_tk <= 2048)
       hipLaunchKernelGGL((attn_decode_stream_kernel<2048, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a, pos);
     else
