@@ -329,6 +329,7 @@ class DecoderRunner:
         self.hist_cols = max_steps or decoder.n_ctx
         self.history = torch.zeros((batch, self.hist_cols), dtype=torch.int64, device=dev)
         self.graph = None
+        self.graph_multi = None  # GRAPH_STEPS steps in one graph
         self.graph_stream = None
         self.prev0 = torch.zeros(batch, dtype=torch.int64, device=dev)  # the prompt's last token
         self.filters = filters
@@ -537,6 +538,11 @@ class DecoderRunner:
                       *_pf_args(nxt), _stream())
             f2.linear32_res(f8f, B, x16, sc["m"])
 
+    # Steps per replay of the multi-step graph: every graph launch leaves a
+    # gap of ~9 us before its first kernel, so n steps run as n // 8 replays of
+    # an 8-step graph and the rest as replays of the one-step graph.
+    GRAPH_STEPS = 8
+
     def _replay(self, n: int):
         if n <= 0:
             return
@@ -557,6 +563,16 @@ class DecoderRunner:
             with torch.cuda.graph(g, stream=s):
                 self.decode_step()
             self.graph, self.graph_stream = g, s
+        if n >= self.GRAPH_STEPS and self.graph_multi is None:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.graph_stream):
+                for _ in range(self.GRAPH_STEPS):
+                    self.decode_step()
+            self.graph_multi = g
+        if self.graph_multi is not None:
+            for _ in range(n // self.GRAPH_STEPS):
+                self.graph_multi.replay()
+            n %= self.GRAPH_STEPS
         for _ in range(n):
             self.graph.replay()
 
