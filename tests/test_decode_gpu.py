@@ -246,3 +246,25 @@ def test_graph_replay_matches_eager_and_oracle(iw, gpu, tiny_model):
         assert np.array_equal(host(g_toks), host(e_toks)), f"utterance {seed}"
         r_toks = ref.greedy(ref.encoder(mel), prompt, steps)
         assert np.array_equal(host(g_toks), r_toks), f"utterance {seed}"
+
+
+def test_weight_prefetch_does_not_change_results(iw, gpu, tiny_model):
+    """The one-token step with and without the next-GEMM weight prefetch (the
+    LayerNorms and FC1 reading the next GEMM's weight tiles into L2): the same
+    greedy tokens, replayed from graphs of 8 steps and of one step, and the
+    same logits step by step."""
+    dims, params = tiny_model
+    model = iw.Whisper_int.from_params(dims, params).cuda()
+    B, steps = 5, 19  # 18 replayed steps: two 8-step graphs and two one-step replays
+    mel = iw.synth.synthetic_mel(B, dims.n_mels, 2 * dims.n_audio_ctx, seed=7)
+    prompt = np.random.default_rng(7).integers(0, dims.n_vocab, size=(B, 3)).astype(np.int64)
+    runners = [iw.DecoderRunner(model.decoder, B, dims.n_audio_ctx, prefetch=pf) for pf in (False, True)]
+    eager = [iw.DecoderRunner(model.decoder, B, dims.n_audio_ctx, use_graph=False, prefetch=pf)
+             for pf in (False, True)]
+    with torch.no_grad():
+        feats = model.embed_audio(T(mel))
+        toks = [host(iw.greedy_decode(model, feats, T(prompt), steps, runner=r)) for r in runners]
+        logits = [host(iw.greedy_decode(model, feats, T(prompt), steps, runner=r, keep_logits=True)[1])
+                  for r in eager]
+    assert np.array_equal(toks[0], toks[1])
+    assert np.array_equal(logits[0], logits[1])
