@@ -40,14 +40,19 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, TOP/s
 HBM_PEAK_GBS = 8000.0
 
 WORKLOADS = {
-    # name: (shape, batch, decode steps, description)
-    "large": ("large", 128, 445, "Whisper-large shapes (d=1280, 20 heads, 32+32 layers, 128 mels), "
+    # name: (shape, batch, decode steps, prompt seed (None = the Whisper start
+    # prompt), description)
+    "large": ("large", 128, 445, None, "Whisper-large shapes (d=1280, 20 heads, 32+32 layers, 128 mels), "
               "integer encoder + greedy decoder, batch 128, 445 greedy steps after a 3-token prompt "
               "(448-token context)"),
-    "medium": ("medium", 64, 221, "Whisper-medium shapes, batch 64, 221 greedy steps"),
-    "small": ("small", 32, 128, "Whisper-small shapes, batch 32, 128 greedy steps"),
-    "base-encoder": ("base", 16, 0, "Whisper-base shapes, integer encoder only, batch 16"),
-    "tiny": ("tiny", 1, 32, "Whisper-tiny shapes (4 heads), batch 1, 32 greedy steps"),
+    "medium": ("medium", 64, 224, 4, "Whisper-medium shapes (d=1024, 16 heads, 24+24 layers), batch 64, "
+               "224 greedy steps after 3 seeded uniform random prompt ids in [0, 51865)"),
+    "small": ("small", 32, 128, None, "Whisper-small shapes (d=768, 12 heads, 12+12 layers), batch 32, "
+              "128 greedy steps"),
+    "base-encoder": ("base", 16, 0, None, "Whisper-base shapes (d=512, 8 heads, 6 layers), integer "
+                     "encoder only, batch 16"),
+    "tiny": ("tiny", 1, 32, None, "Whisper-tiny shapes (d=384, 4 heads, 4+4 layers), batch 1, 32 greedy "
+             "steps"),
 }
 
 
@@ -225,7 +230,7 @@ def main():
     import __graft_entry__
 
     iw = __graft_entry__.load_package()
-    shape, batch, dsteps, desc = WORKLOADS[args.workload]
+    shape, batch, dsteps, prompt_seed, desc = WORKLOADS[args.workload]
     batch = args.batch or batch
     dsteps = dsteps if args.decode_steps is None else args.decode_steps
     dims = iw.SHAPES[shape]
@@ -239,7 +244,7 @@ def main():
         f"in {time.time() - t0:.1f} s")
     model = iw.Whisper_int.from_params(dims, params).cuda().eval()
     mel = torch.from_numpy(iw.synth.synthetic_mel(batch, dims.n_mels, 2 * dims.n_audio_ctx, seed=1)).cuda()
-    prompt = torch.from_numpy(iw.synth.prompt_tokens(batch, dims.n_vocab)).cuda()
+    prompt = torch.from_numpy(iw.synth.prompt_tokens(batch, dims.n_vocab, seed=prompt_seed)).cuda()
     enc = iw.EncoderRunner(model.encoder, batch)
     dec = iw.DecoderRunner(model.decoder, batch, dims.n_audio_ctx) if dsteps else None
     torch.cuda.synchronize()

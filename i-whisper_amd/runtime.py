@@ -8,13 +8,19 @@ chosen for the MI355X instead of the reference's per-call tensors:
   bias in the concatenation.
 * The residual stream is one int16 buffer updated in place by the fused
   Linear32 + residual15 kernels.
-* The decoder keeps preallocated KV caches: self-attention K as [B, n_ctx, C]
-  and V transposed per head [B, H, D, n_ctx]; cross-attention K/V are
-  projected once per utterance. This replaces the reference's hook-based
-  ``torch.cat`` cache (model_int.py:1587-1618) with identical values.
+* The decoder keeps preallocated per-head KV caches: self-attention K as
+  [B, H, n_ctx, D] and V transposed per head [B, H, D, n_ctx16];
+  cross-attention K/V likewise, projected once per utterance. This replaces
+  the reference's hook-based ``torch.cat`` cache (model_int.py:1587-1618) with
+  identical values.
 * Greedy decoding feeds the last token each step (decoding.py:148-179,
-  684-712) and takes the first maximum of the int8 logits, a fixed number of
-  steps with no logit filters.
+  684-712) and takes the first maximum of the int8 logits for a fixed number
+  of steps, optionally after the decoding task's logit filters
+  (``LogitFilters``, applied on the device).
+
+The runners copy (and for the one-token step, repack) the model's weights
+when they are built: a runner built before ``load_state_dict`` keeps the old
+weights, so build a new runner after loading new weights.
 """
 from __future__ import annotations
 
@@ -225,6 +231,11 @@ class EncoderRunner:
         self._tock(t)
 
     def __call__(self, mel: torch.Tensor) -> torch.Tensor:
+        want = (self.B, self.enc.n_mels, 2 * self.T)
+        if tuple(mel.shape) != want:
+            raise ValueError(f"mel batch of shape {tuple(mel.shape)}; this runner takes {want}")
+        if mel.dtype not in (torch.float32, torch.int8):
+            raise ValueError(f"mel must be float32 or int8, not {mel.dtype}")
         x16 = self.enc.frontend(mel)
         for i in range(len(self.enc.blocks)):
             self.block(i, x16)
@@ -351,6 +362,11 @@ class DecoderRunner:
     # ---- per utterance ----
     def set_audio(self, xa: torch.Tensor):
         """Project the cross-attention K/V of the encoder output once per utterance."""
+        want = (self.B, self.Ta, self.C)
+        if tuple(xa.shape) != want or xa.dtype != torch.int8:
+            raise ValueError(f"audio features {tuple(xa.shape)} {xa.dtype}; this runner takes int8 {want}")
+        if not xa.is_cuda:
+            raise ValueError("audio features must be on the GPU")
         xa = xa.contiguous()
         B, Ta, C, H, D = self.B, self.Ta, self.C, self.H, self.D
         kv = self.kv_tmp
@@ -578,6 +594,14 @@ class DecoderRunner:
 
     def run(self, prompt: torch.Tensor, steps: int, keep_logits: bool = False):
         """Greedy tokens [B, steps] after ``prompt`` (and the int8 logits of every step)."""
+        if prompt.dim() != 2 or prompt.shape[0] != self.B or prompt.shape[1] < 1:
+            raise ValueError(f"prompt of shape {tuple(prompt.shape)}; this runner takes [{self.B}, P >= 1]")
+        if prompt.dtype != torch.int64 or not prompt.is_cuda:
+            raise ValueError("prompt must be an int64 tensor on the GPU")
+        if steps < 1:
+            raise ValueError("steps must be at least 1")
+        if prompt.shape[1] + steps > self.Tcap:
+            raise ValueError(f"prompt + steps exceeds n_text_ctx ({self.Tcap})")
         if steps > self.hist_cols:
             raise ValueError("more steps than the history holds")
         self.reset()
@@ -595,6 +619,28 @@ class DecoderRunner:
         if keep_logits:
             return toks, torch.stack(logits, 1)
         return toks
+
+    def run_forced(self, prompt: torch.Tensor, forced: torch.Tensor):
+        """Teacher-forced steps: the prompt step, then one step per column of
+        ``forced`` [B, n] fed as the next input token instead of the previous
+        step's choice (eager launches). Returns the first-index argmax of every
+        step's int8 logits [B, n + 1] and those logits [B, n + 1, vocab]."""
+        if self.filters is not None:
+            raise ValueError("teacher forcing takes a runner built without logit filters")
+        if forced.dim() != 2 or forced.shape[0] != self.B or forced.dtype != torch.int64:
+            raise ValueError(f"forced tokens must be int64 [{self.B}, n]")
+        n = forced.shape[1]
+        if n + 1 > self.hist_cols or prompt.shape[1] + n > self.Tcap:
+            raise ValueError("too many forced steps for this runner")
+        if n and (int(forced.min()) < 0 or int(forced.max()) >= self.dec.n_vocab):
+            raise ValueError("forced token id out of range")
+        self.run(prompt, 1, keep_logits=True)
+        logits = [self.logits.clone()]
+        for i in range(n):
+            self.tokens.copy_(forced[:, i])
+            self.decode_step()
+            logits.append(self.logits.clone())
+        return self.history[:, :n + 1].clone(), torch.stack(logits, 1)
 
 
 def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torch.Tensor,
@@ -615,8 +661,9 @@ def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torc
     if runner is None:
         runner = DecoderRunner(dec, B, audio_features.shape[1], use_graph=not keep_logits,
                                filters=filters)
-    elif filters is not None and runner.filters is not filters:
-        raise ValueError("the runner was built with other logit filters")
+    elif runner.filters is not filters:
+        raise ValueError("the runner was built with other logit filters (pass the runner's own "
+                         "filters, or None for a runner built without filters)")
     runner.set_audio(audio_features)
     res = runner.run(prompt, steps, keep_logits=keep_logits)
     if keep_logits:

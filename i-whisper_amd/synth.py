@@ -65,7 +65,11 @@ class _Gen:
         return torch.from_numpy(a)
 
 
-def float_weights(dims: ModelDimensions, seed: int) -> Dict[str, torch.Tensor]:
+def float_weights(dims: ModelDimensions, seed: int, decoder_mlp_scale: float = 1.0) -> Dict[str, torch.Tensor]:
+    """Random-init float weights. ``decoder_mlp_scale`` scales the decoder MLPs'
+    output weights and FC1 biases (1 = plain N(0, 0.02)): a random decoder's
+    MLP adds the same direction to every position, so its greedy argmax hardly
+    depends on the input; a small scale lets the argmax follow the input."""
     g = _Gen(seed)
     W: Dict[str, torch.Tensor] = {}
     d, dt = dims.n_audio_state, dims.n_text_state
@@ -97,6 +101,9 @@ def float_weights(dims: ModelDimensions, seed: int) -> Dict[str, torch.Tensor]:
     W["decoder.positional_embedding"] = g.normal(dims.n_text_ctx, dt)
     for i in range(dims.n_text_layer):
         block(f"decoder.blocks.{i}", dt, True)
+        if decoder_mlp_scale != 1.0:
+            for k in ("mlp.0.bias", "mlp.2.weight", "mlp.2.bias"):
+                W[f"decoder.blocks.{i}.{k}"] *= decoder_mlp_scale
     W["decoder.ln.weight"] = torch.ones(dt)
     W["decoder.ln.bias"] = torch.zeros(dt)
     return W
@@ -370,12 +377,14 @@ def _blocks(W, P, st, prefix: str, n_layer: int, n_head: int, x_alpha: float, cr
     return x_alpha
 
 
-def calibrated_int_params(dims: ModelDimensions, seed: int = 0, n_calib: int = 2,
+def calibrated_int_params(dims: ModelDimensions, seed: int = 0, n_calib: int = 8,
                           calib_ctx: Optional[int] = None, calib_tokens: int = 16,
-                          verbose: bool = False) -> Dict[str, np.ndarray]:
-    """Integer parameters of ``Whisper_int`` (reference state-dict keys and dtypes)."""
+                          verbose: bool = False, decoder_mlp_scale: float = 1.0) -> Dict[str, np.ndarray]:
+    """Integer parameters of ``Whisper_int`` (reference state-dict keys and dtypes),
+    calibrated on ``n_calib`` seeded mels of 2 * min(n_audio_ctx, calib_ctx or 300)
+    frames."""
     torch_threads = torch.get_num_threads()
-    W = float_weights(dims, seed)
+    W = float_weights(dims, seed, decoder_mlp_scale)
     ctx = min(dims.n_audio_ctx, calib_ctx or 300)
     mels = torch.from_numpy(synthetic_mel(n_calib, dims.n_mels, 2 * ctx, seed + 1))
     toks = np.concatenate([prompt_tokens(n_calib, dims.n_vocab),

@@ -155,3 +155,17 @@ class OracleWhisper:
         if return_logits:
             return tokens, np.stack(last, 1)
         return tokens
+
+    def forced(self, xa, prompt, forced):
+        """Teacher-forced decoding over the cache: the prompt step, then one step
+        per column of ``forced`` [B, n] fed as the next input token. Returns the
+        argmax of every step's last-position int8 logits [B, n + 1] and those
+        logits [B, n + 1, vocab]."""
+        tokens = np.array(prompt, dtype=np.int64)
+        forced = np.asarray(forced, dtype=np.int64)
+        cache = {}
+        last = [self.decoder_logits(tokens, xa, cache)[:, -1]]
+        for i in range(forced.shape[1]):
+            last.append(self.decoder_logits(forced[:, i:i + 1], xa, cache)[:, -1])
+        logits = np.stack(last, 1)
+        return np.argmax(logits, axis=-1).astype(np.int64), logits

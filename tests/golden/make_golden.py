@@ -281,21 +281,30 @@ def model_tiny():
     dims = iw.ModelDimensions(n_mels=80, n_audio_ctx=100, n_audio_state=384, n_audio_head=4,
                               n_audio_layer=1, n_vocab=1000, n_text_ctx=48, n_text_state=384,
                               n_text_head=4, n_text_layer=1)
-    params = iw.synth.calibrated_int_params(dims, seed=4321, calib_ctx=100)
+    # decoder MLP outputs scaled down so that the argmax follows the input
+    params = iw.synth.calibrated_int_params(dims, seed=4321, calib_ctx=100, decoder_mlp_scale=0.1)
     mel = iw.synth.synthetic_mel(2, dims.n_mels, 2 * dims.n_audio_ctx, seed=77)
     ref = OracleWhisper(dims, params, kind="ref")
     x = ref.encoder_input(mel)
     feats = ref.encoder(x)
-    prompt = iw.synth.prompt_tokens(2, dims.n_vocab)
+    # a different seeded random prompt per row
+    prompt = iw.synth.prompt_tokens(2, dims.n_vocab, seed=78)
     toks, logits = ref.greedy(feats, prompt, 12, return_logits=True)
+    # teacher-forced steps: 16 seeded random input tokens per row fed through
+    # the cache, so that the inputs, and with them the argmax ids, vary from
+    # step to step (greedy decoding of a random-weight model repeats a token)
+    forced = np.random.default_rng(79).integers(0, dims.n_vocab, size=(2, 16)).astype(np.int64)
+    f_argmax, f_logits = ref.forced(feats, prompt, forced)
     out = {"dims": np.array([dims.n_mels, dims.n_audio_ctx, dims.n_audio_state, dims.n_audio_head,
                              dims.n_audio_layer, dims.n_vocab, dims.n_text_ctx, dims.n_text_state,
                              dims.n_text_head, dims.n_text_layer], np.int64),
-           "mel_int8": x, "encoder_out": feats, "prompt": prompt, "tokens": toks, "logits": logits}
+           "mel_int8": x, "encoder_out": feats, "prompt": prompt, "tokens": toks, "logits": logits,
+           "forced": forced, "forced_argmax": f_argmax, "forced_logits": f_logits}
     for k, v in params.items():
         out["param." + k] = v
     np.savez_compressed(HERE / "model_tiny.npz", **out)
-    print(f"model_tiny: tokens {toks.tolist()}, {(HERE / 'model_tiny.npz').stat().st_size} bytes")
+    print(f"model_tiny: tokens {toks.tolist()}, forced argmax {f_argmax.tolist()}, "
+          f"{(HERE / 'model_tiny.npz').stat().st_size} bytes")
 
 
 def main():
@@ -319,4 +328,9 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    import sys
+
+    if sys.argv[1:] == ["model_tiny"]:  # only the end-to-end fixture
+        model_tiny()
+    else:
+        main()

@@ -255,7 +255,9 @@ def test_weight_prefetch_does_not_change_results(iw, gpu, tiny_model):
     same logits step by step."""
     dims, params = tiny_model
     model = iw.Whisper_int.from_params(dims, params).cuda()
-    B, steps = 5, 19  # 18 replayed steps: two 8-step graphs and two one-step replays
+    # 18 steps after the prompt: one eager warm-up step before capture, two
+    # replays of the 8-step graph and one replay of the one-step graph
+    B, steps = 5, 19
     mel = iw.synth.synthetic_mel(B, dims.n_mels, 2 * dims.n_audio_ctx, seed=7)
     prompt = np.random.default_rng(7).integers(0, dims.n_vocab, size=(B, 3)).astype(np.int64)
     runners = [iw.DecoderRunner(model.decoder, B, dims.n_audio_ctx, prefetch=pf) for pf in (False, True)]

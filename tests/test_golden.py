@@ -215,6 +215,17 @@ def test_oracle_model_matches_golden(iw):
     toks, logits = o.greedy(feats, z["prompt"], z["logits"].shape[1], return_logits=True)
     assert np.array_equal(logits, z["logits"])
     assert np.array_equal(toks, z["tokens"])
+    f_argmax, f_logits = o.forced(feats, z["prompt"], z["forced"])
+    assert np.array_equal(f_logits, z["forced_logits"])
+    assert np.array_equal(f_argmax, z["forced_argmax"])
+
+
+def test_model_fixture_exercises_token_ids(iw):
+    """Each row has its own prompt, and the teacher-forced steps' argmax ids vary."""
+    dims, params, z = model_fixture(iw)
+    assert not np.array_equal(z["prompt"][0], z["prompt"][1])
+    assert all(len(np.unique(r)) >= 6 for r in z["forced_argmax"])
+    assert z["forced_argmax"].max() >= 0 and z["forced_argmax"].max() < dims.n_vocab
 
 
 def test_golden_fixtures_are_not_degenerate():
@@ -255,3 +266,12 @@ def test_hip_model_matches_golden(iw, gpu):
     assert np.array_equal(feats.cpu().numpy(), z["encoder_out"])
     assert np.array_equal(logits.cpu().numpy(), z["logits"])
     assert np.array_equal(toks.cpu().numpy(), z["tokens"])
+    # teacher-forced steps through the runner's one-token step
+    for frag in (True, False):
+        run = iw.DecoderRunner(model.decoder, 2, dims.n_audio_ctx, use_graph=False, frag=frag)
+        with torch.no_grad():
+            run.set_audio(feats)
+            f_argmax, f_logits = run.run_forced(torch.from_numpy(z["prompt"]).cuda(),
+                                                torch.from_numpy(z["forced"]).cuda())
+        assert np.array_equal(f_logits.cpu().numpy(), z["forced_logits"]), frag
+        assert np.array_equal(f_argmax.cpu().numpy(), z["forced_argmax"]), frag

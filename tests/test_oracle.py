@@ -321,3 +321,29 @@ def test_layernorm_invariants(oracle):
         out = oracle.layernorm32(x, g, b, 128, 10, 0x80000000, 0)
         exp = np.clip([_rshift_closed((int(v) * 0x80000000) >> 32, 0) for v in b], -127, 127)
         assert np.array_equal(out[0], np.array(exp, np.int8))
+
+
+def test_model_oracle_cached_steps_equal_one_causal_pass(iw):
+    """The decoder over the cache, one token per step (model_int.py:1398-1442 with
+    the hook cache of :1587-1618), gives at every step the logits that one causal
+    pass over the whole token sequence gives at that position (the mask slice
+    mask[k_len - q_len : k_len, :k_len] of model_int.py:794-797 leaves query t
+    the keys 0 .. t either way). The workload parity tests rely on this."""
+    from oracle.model_oracle import OracleWhisper
+
+    dims = iw.ModelDimensions(n_mels=80, n_audio_ctx=40, n_audio_state=384, n_audio_head=6,
+                              n_audio_layer=1, n_vocab=300, n_text_ctx=24, n_text_state=384,
+                              n_text_head=6, n_text_layer=2)
+    P = iw.synth.calibrated_int_params(dims, seed=8, decoder_mlp_scale=0.1)
+    o = OracleWhisper(dims, P, threads=4)
+    xa = o.encoder(iw.synth.synthetic_mel(2, 80, 80, seed=9))
+    prompt = np.array([[5, 17, 200], [9, 9, 31]], np.int64)
+    toks, step_logits = o.greedy(xa, prompt, 10, return_logits=True)
+    full = o.decoder_logits(toks[:, :-1], xa)
+    assert np.array_equal(full[:, 2:], step_logits)
+    # teacher forcing through the cache agrees with the causal pass as well
+    forced = np.random.default_rng(3).integers(0, 300, size=(2, 9))
+    f_argmax, f_logits = o.forced(xa, prompt, forced)
+    full = o.decoder_logits(np.concatenate([prompt, forced], 1), xa)
+    assert np.array_equal(full[:, 2:], f_logits)
+    assert np.array_equal(f_argmax, full[:, 2:].argmax(-1))
