@@ -57,6 +57,7 @@ SIGNATURES = {
     "iw_embed_tokens": [_p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _p],
     "iw_greedy_advance": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p],
     "iw_log_mel": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64, _p, _p],
+    "iw_log_mel_noalloc": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _i32, _p, _i64, _p],
     "iw_dtw": [_p, _i64, _i64, _i64, _p, _i64, _p],
     "iw_median_filter": [_p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "iw_greedy_advance_filtered": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p, _p, _p,
@@ -76,7 +77,8 @@ SIGNATURES = {
 }
 
 # entry points that return a value rather than a status
-VALUE_FUNCS = {"iw_frag_bytes": ([_i64, _i64], C.c_int64)}
+VALUE_FUNCS = {"iw_frag_bytes": ([_i64, _i64], C.c_int64),
+               "iw_log_mel_scratch_floats": ([_i64, _i64], C.c_int64)}
 
 _lock = threading.Lock()
 _lib = None

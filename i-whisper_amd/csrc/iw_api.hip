@@ -209,6 +209,26 @@ int frag_prefetch_args(const int8_t *next_weight, int64_t next_n, int64_t next_k
   return IW_OK;
 }
 
+
+// argument checks shared by iw_log_mel and iw_log_mel_noalloc (workspace
+// excluded)
+int check_log_mel(const float *audio, int64_t batch, int64_t n_samples, int64_t audio_ld,
+                  const float *twiddle, const float *window, const int32_t *filter_start,
+                  const int32_t *filter_len, const int32_t *filter_offset, const float *filter_weights,
+                  int32_t n_taps, int32_t n_mels, const float *out, int64_t out_batch_stride) {
+  int max_mels = 0, max_taps = 0;
+  log_mel_limits(&max_mels, &max_taps);
+  IW_REQUIRE(batch >= 0 && n_samples > 256 && n_samples / 160 < (1 << 30) && audio_ld >= n_samples,
+             "invalid audio shape (more than 256 samples per row)");
+  IW_REQUIRE(n_mels > 0 && n_mels <= max_mels, "n_mels must be in 1 .. 128");
+  IW_REQUIRE(n_taps >= 0 && n_taps <= max_taps, "too many filterbank taps");
+  IW_REQUIRE(out_batch_stride >= (int64_t)n_mels * (n_samples / 160), "output batch stride too small");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(audio && twiddle && window && filter_start && filter_len && filter_offset && out &&
+                 (n_taps == 0 || filter_weights),
+             "null tensor pointer");
+  return IW_OK;
+}
 }  // namespace
 }  // namespace iw
 
@@ -706,23 +726,43 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                      timestamp_begin, max_initial_timestamp, logit_scale, as_stream(stream));
 }
 
+
 int iw_log_mel(const float *audio, int64_t batch, int64_t n_samples, int64_t audio_ld, const float *twiddle,
                const float *window, const int32_t *filter_start, const int32_t *filter_len,
                const int32_t *filter_offset, const float *filter_weights, int32_t n_taps, int32_t n_mels,
                float *out, int64_t out_batch_stride, float *workspace, iw_stream_t stream) {
-  int max_mels = 0, max_taps = 0;
-  log_mel_limits(&max_mels, &max_taps);
-  IW_REQUIRE(batch >= 0 && n_samples > 256 && n_samples / 160 < (1 << 30) && audio_ld >= n_samples,
-             "invalid audio shape (more than 256 samples per row)");
-  IW_REQUIRE(n_mels > 0 && n_mels <= max_mels, "n_mels must be in 1 .. 128");
-  IW_REQUIRE(n_taps >= 0 && n_taps <= max_taps, "too many filterbank taps");
-  IW_REQUIRE(out_batch_stride >= (int64_t)n_mels * (n_samples / 160), "output batch stride too small");
-  if (batch == 0) return IW_OK;
-  IW_REQUIRE(audio && twiddle && window && filter_start && filter_len && filter_offset && out && workspace &&
-                 (n_taps == 0 || filter_weights),
-             "null tensor pointer");
+  int rc = check_log_mel(audio, batch, n_samples, audio_ld, twiddle, window, filter_start, filter_len,
+                         filter_offset, filter_weights, n_taps, n_mels, out, out_batch_stride);
+  if (rc != IW_OK || batch == 0) return rc;
+  IW_REQUIRE(workspace, "null tensor pointer");
   return launch_log_mel(audio, batch, n_samples, audio_ld, twiddle, window, filter_start, filter_len,
                         filter_offset, filter_weights, n_taps, n_mels, out, out_batch_stride, workspace,
+                        as_stream(stream));
+}
+
+int64_t iw_log_mel_scratch_floats(int64_t batch, int64_t n_samples) {
+  if (batch < 0 || n_samples < 0) return -1;
+  return batch * ((n_samples / 160 + 63) / 64);
+}
+
+int iw_log_mel_noalloc(const float *audio, int64_t batch, int64_t n_samples, int64_t audio_ld,
+                       const float *twiddle, const float *window, const int32_t *filter_start,
+                       const int32_t *filter_len, const int32_t *filter_offset, const float *filter_weights,
+                       int32_t n_taps, int32_t n_mels, float *out, int64_t out_batch_stride,
+                       iw_stream_t stream) {
+  int rc = check_log_mel(audio, batch, n_samples, audio_ld, twiddle, window, filter_start, filter_len,
+                         filter_offset, filter_weights, n_taps, n_mels, out, out_batch_stride);
+  if (rc != IW_OK || batch == 0) return rc;
+  IW_REQUIRE(iw_log_mel_scratch_floats(batch, n_samples) <= IW_LOG_MEL_SCRATCH_FLOATS,
+             "iw_log_mel_noalloc: batch * ceil((n_samples / 160) / 64) exceeds the fixed scratch of "
+             "IW_LOG_MEL_SCRATCH_FLOATS (65536) block maxima; use iw_log_mel with a workspace");
+  float *blockmax = nullptr;
+  rc = log_mel_scratch(as_stream(stream), &blockmax);
+  if (rc != IW_OK) return rc;
+  // every block of the transform kernel writes its own maximum before the
+  // finishing kernel reads it, so nothing needs clearing between calls
+  return launch_log_mel(audio, batch, n_samples, audio_ld, twiddle, window, filter_start, filter_len,
+                        filter_offset, filter_weights, n_taps, n_mels, out, out_batch_stride, blockmax,
                         as_stream(stream));
 }
 

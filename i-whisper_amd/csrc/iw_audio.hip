@@ -2,10 +2,48 @@
 // frames of a periodic Hann window with reflect padding, |X|^2, the mel
 // filterbank, log10 of max(., 1e-10); then per audio the floor
 // max(log, max_all - 8) and log / 4 + 1.
+#include "../../include/iwhisper_amd.h"
 #include "iw_common.hpp"
 #include "iw_kernels.hpp"
 
+#include <mutex>
+
+// Block maxima of iw_log_mel_noalloc: a fixed device array instead of a
+// caller workspace, for callers that cannot allocate. Each GPU holds its own
+// copy (at its own address, looked up once per device below) until the process
+// ends; every call on one GPU shares it, so calls that overlap on one GPU race.
+static __device__ __align__(256) float scratch[IW_LOG_MEL_SCRATCH_FLOATS];
+
 namespace iw {
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxScratchDevices] = {};
+}  // namespace
+
+int log_mel_scratch(hipStream_t stream, float **ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail("iw_log_mel_noalloc: no usable current device");
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev)
+      return fail("iw_log_mel_noalloc: the stream does not belong to the current device");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    // device address of this device's copy (the host-side name `scratch` is
+    // not a device address and is never passed to a kernel)
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(std::string("iw_log_mel_noalloc: hipGetSymbolAddress failed: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float *>(p);
+  }
+  *ptr = g_scratch_ptr[dev];
+  return IW_OK;
+}
 
 namespace {
 

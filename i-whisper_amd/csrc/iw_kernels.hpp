@@ -64,6 +64,9 @@ int launch_log_mel(const float *audio, int64_t batch, int64_t n_samples, int64_t
                    const float *window, const int *fstart, const int *flen, const int *foff, const float *fw,
                    int n_taps, int n_mels, float *out, int64_t out_ld_b, float *blockmax, hipStream_t s);
 int log_mel_limits(int *max_mels, int *max_taps);
+// this device's IW_LOG_MEL_SCRATCH_FLOATS-float block-maxima array (the
+// stream must belong to the current device)
+int log_mel_scratch(hipStream_t stream, float **ptr);
 int launch_dtw(const float *x, int64_t M, int64_t N, int64_t ld, int8_t *trace, int64_t tld, hipStream_t s);
 int launch_median_filter(const float *x, int64_t rows, int64_t cols, int64_t ld, int32_t width, float *y,
                          int64_t ldy, hipStream_t s);

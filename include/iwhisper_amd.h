@@ -415,6 +415,29 @@ int iw_log_mel(const float *audio, int64_t batch, int64_t n_samples, int64_t aud
                const int32_t *filter_offset, const float *filter_weights, int32_t n_taps, int32_t n_mels,
                float *out, int64_t out_batch_stride, float *workspace, iw_stream_t stream);
 
+/* Block-maximum entries of iw_log_mel's workspace for batch rows of n_samples
+ * samples: batch * ceil((n_samples / 160) / 64) (-1 for negative sizes). */
+int64_t iw_log_mel_scratch_floats(int64_t batch, int64_t n_samples);
+
+/* Maximum iw_log_mel_scratch_floats() that iw_log_mel_noalloc takes (256 KB of
+ * float block maxima per GPU: 1394 rows of 30 s audio). */
+#define IW_LOG_MEL_SCRATCH_FLOATS 65536
+
+/* iw_log_mel without the workspace argument, allocating nothing: no
+ * counterpart in the reference. For callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). The block maxima live in a fixed device array of
+ * IW_LOG_MEL_SCRATCH_FLOATS floats that each GPU holds from its first call until
+ * the process ends; larger inputs are rejected (IW_EINVAL). Every call on one
+ * GPU shares that array, so calls that overlap on one GPU (several streams or
+ * threads) race; calls in order on one stream do not. The stream must belong to
+ * the current device. Results equal iw_log_mel's. */
+int iw_log_mel_noalloc(const float *audio, int64_t batch, int64_t n_samples, int64_t audio_ld,
+                       const float *twiddle, const float *window, const int32_t *filter_start,
+                       const int32_t *filter_len, const int32_t *filter_offset,
+                       const float *filter_weights, int32_t n_taps, int32_t n_mels, float *out,
+                       int64_t out_batch_stride, iw_stream_t stream);
+
 /* Dynamic time warping for word timestamps (triton_ops.py:13-40, dtw_cuda
  * timing.py:108-141; it replaces the Triton kernel launch): over float32 costs
  * x [rows][cols] (row stride ld; rows < 1024, the reference's M < BLOCK_SIZE),
