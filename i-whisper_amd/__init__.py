@@ -11,7 +11,7 @@ from .model_int import (  # noqa: F401
     ResidualAttentionBlock_int, TextDecoder_int, Whisper_int, set_all_backends,
     set_attention_backend, set_conv1d_backend, set_decoder_backend, set_encoder_backend,
     set_gelu_backend, set_layernorm_backend, set_residual_backend)
-from .runtime import DecoderRunner, EncoderRunner, LogitFilters, greedy_decode  # noqa: F401
+from .runtime import DecoderRunner, EncoderRunner, GreedyResult, LogitFilters, greedy_decode  # noqa: F401
 from . import audio, checkpoint, timing  # noqa: F401
 from .checkpoint import (  # noqa: F401
     load_int_model, load_int_params, save_int_model, verify_int_model_roundtrip)

@@ -61,7 +61,11 @@ SIGNATURES = {
     "iw_dtw": [_p, _i64, _i64, _i64, _p, _i64, _p],
     "iw_median_filter": [_p, _i64, _i64, _i64, _i32, _p, _i64, _p],
     "iw_greedy_advance_filtered": [_p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _p, _p, _p,
-                                   _i32, _i32, _i32, _f, _p],
+                                   _i32, _i32, _i32, _f, _p, _p, _p],
+    "iw_greedy_update": [_p, _i64, _p, _i64, _i64, _i64, _p, _p, _i64, _i64, _p, _p, _i32, _i32, _p, _p, _f,
+                         _p, _p, _p],
+    "iw_token_prob": [_p, _i64, _i64, _i64, _i64, _f, _p, _p],
+    "iw_classifier_argmax_frag": [_p, _p, _u32, _i8, _p, _p, _i64, _i64, _i64, _p],
     "iw_frag_pack": [_p, _i64, _i64, _i64, _p, _p],
     "iw_linear8_frag": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _b, _b, _b, _p],
     "iw_linear8_gelu_frag": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64,

@@ -714,16 +714,46 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                int32_t pos_increment, const uint32_t *suppress,
                                const uint32_t *suppress_first, const int64_t *prev0, int32_t eot,
                                int32_t timestamp_begin, int32_t max_initial_timestamp,
-                               float logit_scale, iw_stream_t stream) {
+                               float logit_scale, float *sum_logprobs, int32_t *eot_count,
+                               iw_stream_t stream) {
   IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 23) && ld >= cols && history_cols > 0 &&
                  history_ld >= history_cols,
              "invalid greedy step shape (at most 2^23 - 1 columns)");
   IW_REQUIRE(logits && next_tokens && history && step && pos, "null tensor pointer");
   IW_REQUIRE(timestamp_begin < 0 || eot >= 0, "the timestamp rules need the EOT id");
-  IW_REQUIRE(timestamp_begin < 0 || logit_scale > 0.f, "logit_scale must be positive");
+  IW_REQUIRE((timestamp_begin < 0 && !sum_logprobs) || logit_scale > 0.f, "logit_scale must be positive");
   return launch_greedy_step_filtered(logits, rows, cols, ld, next_tokens, history, history_ld, history_cols,
                                      step, pos, pos_increment, suppress, suppress_first, prev0, eot,
-                                     timestamp_begin, max_initial_timestamp, logit_scale, as_stream(stream));
+                                     timestamp_begin, max_initial_timestamp, logit_scale, sum_logprobs,
+                                     eot_count, as_stream(stream));
+}
+
+int iw_greedy_update(const uint16_t *row_max, int64_t tiles, const int8_t *logits, int64_t ld, int64_t rows,
+                     int64_t cols, int64_t *next_tokens, int64_t *history, int64_t history_ld,
+                     int64_t history_cols, int32_t *step, int32_t *pos, int32_t pos_increment, int32_t eot,
+                     const int64_t *prev0, float *sum_logprobs, float logit_scale, int32_t *eot_count,
+                     uint32_t *arrive, iw_stream_t stream) {
+  IW_REQUIRE(rows >= 0 && rows < (1LL << 31) && cols > 0 && cols < (1 << 23) && history_cols > 0 &&
+                 history_ld >= history_cols,
+             "invalid greedy step shape (at most 2^23 - 1 columns)");
+  IW_REQUIRE(!row_max || tiles == (cols + 31) / 32, "tiles must be ceil(cols / 32)");
+  IW_REQUIRE((row_max || logits) && (!logits || ld >= cols), "the row maxima or the logits are needed");
+  IW_REQUIRE(!sum_logprobs || (logits && logit_scale > 0.f), "log-probabilities need the logits and a positive scale");
+  IW_REQUIRE(next_tokens && history && step && pos && arrive, "null tensor pointer");
+  if (rows == 0) return IW_OK;
+  return launch_greedy_update(row_max, tiles, logits, ld, rows, cols, next_tokens, history, history_ld,
+                              history_cols, step, pos, pos_increment, eot, prev0, sum_logprobs, logit_scale,
+                              eot_count, arrive, as_stream(stream));
+}
+
+int iw_token_prob(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t token, float logit_scale,
+                  float *out, iw_stream_t stream) {
+  IW_REQUIRE(rows >= 0 && cols > 0 && cols < (1 << 30) && ld >= cols, "invalid logits shape");
+  IW_REQUIRE(token >= 0 && token < cols, "token outside the vocabulary");
+  IW_REQUIRE(logit_scale > 0.f, "logit_scale must be positive");
+  if (rows == 0) return IW_OK;
+  IW_REQUIRE(logits && out, "null tensor pointer");
+  return launch_token_prob(logits, rows, cols, ld, token, logit_scale, out, as_stream(stream));
 }
 
 
@@ -909,6 +939,33 @@ int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *
   return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, out, 0, batch, heads,
                                       head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
                                       av_multiplier, av_shift, rsqrt_offset, true, stream);
+}
+
+int iw_classifier_argmax_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift,
+                              int8_t *out, uint16_t *row_max, int64_t M, int64_t K, int64_t N,
+                              iw_stream_t stream) {
+  IW_REQUIRE(K > 0, "hidden size must be positive");
+  IW_REQUIRE(N > 0 && N < (1 << 23), "vocabulary size must be in 1 .. 2^23 - 1");
+  IW_REQUIRE(M >= 0, "invalid row count");
+  if (M == 0) return IW_OK;
+  IW_REQUIRE(x && weight && row_max, "null tensor pointer");
+  int rc = check_frag(x, weight, M, K, N);
+  if (rc) return rc;
+  GemmArgs g;
+  g.a = x;
+  g.b = weight;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.epi = EPI_S8;
+  g.mult_pc = 0;
+  g.out = out;
+  g.ldc = N;
+  g.scalar_mult = multiplier;
+  g.scalar_shift = shift;
+  g.amax = row_max;
+  g.amax_ld = (N + 31) / 32;
+  return gemm_frag(g, nullptr, false, as_stream(stream));
 }
 
 int iw_classifier_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift, int8_t *out,

@@ -75,6 +75,11 @@ struct GemmArgs {
   int64_t out_T = 1;  // OUT_NCT: rows are (b, t) with t in [0, out_T)
   // the next decode GEMM's weight, read into L2 (gemm_frag_kernel only)
   FragPrefetch pf;
+  // per-tensor int8 epilogue (classifier) only, gemm_frag_kernel: the first
+  // maximum of each row within each 32-column tile, amax[m * amax_ld + tile]
+  // = (y + 128) << 5 | (31 - column in tile); out may then be null
+  uint16_t *amax = nullptr;
+  int64_t amax_ld = 0;
 };
 
 // Decode-step QKV projection: the epilogue writes Q (columns [0, C)) to

@@ -26,9 +26,28 @@ using namespace gemm;
 
 namespace {
 
+// Classifier epilogue with the row maxima: the int8 logit of (m, n) as
+// skinny_store's per-tensor form computes it, stored when g.out is set, and
+// the tile's first maximum of row m, reduced over the 32 lanes that hold the
+// row's 32 columns (lanes 0-31 or 32-63 of a wave, column = lane % 32).
+// Padding columns (n >= N) take key 0; every lane takes part.
+__device__ __forceinline__ void classifier_argmax_store(const GemmArgs &g, const ColParams &c, int m, int n,
+                                                        int tile, bool valid, uint32_t a) {
+  uint32_t key = 0;
+  if (valid) {
+    const int32_t y = clampi(apply_shift(mulh_su((int32_t)a, c.mult), c.shift), -127, 127);
+    if (g.out) reinterpret_cast<int8_t *>(g.out)[(int64_t)m * g.ldc + n] = (int8_t)y;
+    key = ((uint32_t)(y + 128) << 5) | (uint32_t)(31 - (n & 31));
+  }
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) key = max(key, (uint32_t)__shfl_xor((int)key, o));
+  if ((threadIdx.x & 31) == 0 && m < (int)g.M) g.amax[(int64_t)m * g.amax_ld + tile] = (uint16_t)key;
+}
+
 // Each wave multiplies the block's 32 x 32 tile over SPW k32 steps; a block
 // has MINW .. MAXW waves (MINW bounds the epilogue rows a thread serves).
-template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, int SPW, int MAXW, int MINW>
+// ARGMAX: the classifier epilogue that also writes the per-tile row maxima.
+template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, int SPW, int MAXW, int MINW, bool ARGMAX = false>
 __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, SkinnyScatter sc, int ms, int tiles,
                                                               int kp) {
   constexpr int PLD = 33;  // LDS row stride of the partial tiles (words)
@@ -118,6 +137,22 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
   __syncthreads();
 
+  if constexpr (ARGMAX) {
+    // all lanes stay for the cross-lane row maxima; a row's 32 columns are
+    // the 32 threads sharing tid / 32
+    const ColParams c = decode_col<EPI>(g, craw);
+#pragma unroll
+    for (int j = 0; j < RMAX; ++j) {
+      const int r = mr0 + mstep * j;
+      const int m = m0 + r;
+      if (r < 32) {  // uniform over each 32-thread group
+        uint32_t a = 0;
+        for (int w = 0; w < nw; ++w) a += (uint32_t)sPart[(w * 32 + r) * PLD + cl];
+        classifier_argmax_store(g, c, m, n, tile, n < N && m < M, a);
+      }
+    }
+    return;
+  }
   if (n >= N) {
     if constexpr (PF) frag_prefetch_keep(pfv);
     return;
@@ -143,7 +178,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
   if constexpr (PF) frag_prefetch_keep(pfv);
 }
 
-template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, int SPW, int MAXW, int MINW>
+template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, int SPW, int MAXW, int MINW, bool ARGMAX = false>
 int launch_frag_waves(const GemmArgs &g, const SkinnyScatter &sc, int64_t kp, hipStream_t s) {
   const int64_t tiles = (g.N + 31) / 32;
   const int ms = (int)((g.M + 31) / 32);
@@ -151,8 +186,8 @@ int launch_frag_waves(const GemmArgs &g, const SkinnyScatter &sc, int64_t kp, hi
   const dim3 grid((unsigned)(((tiles + 7) / 8) * 8 * ms));
   GemmArgs ga = g;
   frag_prefetch_launch(ga.pf, grid.x, 64 * nw);
-  hipLaunchKernelGGL((gemm_frag_kernel<EPI, GELU, SCATTER, OUT_FRAG, SPW, MAXW, MINW>), grid, dim3(64 * nw), 0, s, ga,
-                     sc, ms, (int)tiles, (int)kp);
+  hipLaunchKernelGGL((gemm_frag_kernel<EPI, GELU, SCATTER, OUT_FRAG, SPW, MAXW, MINW, ARGMAX>), grid, dim3(64 * nw),
+                     0, s, ga, sc, ms, (int)tiles, (int)kp);
   return check_launch("gemm_frag_kernel");
 }
 
@@ -160,12 +195,12 @@ int launch_frag_waves(const GemmArgs &g, const SkinnyScatter &sc, int64_t kp, hi
 // weights are in flight, so K is cut into as many wave shares as the block
 // size allows: 5 k32 steps per wave up to Kp = 1280 (<= 8 waves), 10 above
 // (5 .. 16 waves).
-template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG>
+template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, bool ARGMAX = false>
 int launch_frag(const GemmArgs &g, const SkinnyScatter &sc, hipStream_t s) {
   const int64_t kp = frag_kpad(g.K);
-  if (kp <= 1280) return launch_frag_waves<EPI, GELU, SCATTER, OUT_FRAG, 5, 8, 2>(g, sc, kp, s);
-  if (kp <= 2560) return launch_frag_waves<EPI, GELU, SCATTER, OUT_FRAG, 10, 8, 5>(g, sc, kp, s);
-  return launch_frag_waves<EPI, GELU, SCATTER, OUT_FRAG, 10, 16, 9>(g, sc, kp, s);
+  if (kp <= 1280) return launch_frag_waves<EPI, GELU, SCATTER, OUT_FRAG, 5, 8, 2, ARGMAX>(g, sc, kp, s);
+  if (kp <= 2560) return launch_frag_waves<EPI, GELU, SCATTER, OUT_FRAG, 10, 8, 5, ARGMAX>(g, sc, kp, s);
+  return launch_frag_waves<EPI, GELU, SCATTER, OUT_FRAG, 10, 16, 9, ARGMAX>(g, sc, kp, s);
 }
 
 // Row-major [rows][cols] (leading dimension ld) to fragment-major with
@@ -218,6 +253,7 @@ int gemm_frag(const GemmArgs &g, const SkinnyScatter *scatter, bool out_frag, hi
     case EPI_L32RES: return launch_frag<EPI_L32RES, false, false, false>(g, sc, s);
     case EPI_S8:
       if (gelu || out_frag) return fail("the fragment-major classifier has a plain per-tensor epilogue");
+      if (g.amax) return launch_frag<EPI_S8, false, false, false, true>(g, sc, s);
       return launch_frag<EPI_S8, false, false, false>(g, sc, s);
     default: return fail("the fragment-major GEMM has Linear8, Linear32 + residual15 and classifier epilogues");
   }

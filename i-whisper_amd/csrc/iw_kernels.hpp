@@ -74,7 +74,15 @@ int launch_greedy_step_filtered(const int8_t *logits, int64_t rows, int64_t cols
                                 int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
                                 int32_t *pos, int32_t pos_inc, const uint32_t *mask, const uint32_t *mask_first,
                                 const int64_t *prev0, int32_t eot, int32_t ts_begin, int32_t max_init,
-                                float scale, hipStream_t s);
+                                float scale, float *sum_logprobs, int32_t *eot_count, hipStream_t s);
+// GreedyDecoder.update from the classifier's per-tile row maxima (or the
+// logits), with optional log-probability sum, EOT freeze and EOT count
+int launch_greedy_update(const uint16_t *amax, int64_t tiles, const int8_t *logits, int64_t ld, int64_t rows,
+                         int64_t cols, int64_t *next, int64_t *history, int64_t hist_ld, int64_t hist_cols,
+                         int32_t *step, int32_t *pos, int32_t pos_inc, int32_t eot, const int64_t *prev0,
+                         float *sum_logprobs, float scale, int32_t *eot_count, uint32_t *arrive, hipStream_t s);
+int launch_token_prob(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t token, float scale,
+                      float *out, hipStream_t s);
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                        hipStream_t s);
 int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,

@@ -599,6 +599,8 @@ struct GreedyFilter {
   int32_t ts_begin;            // < 0: no timestamp rules
   int32_t max_init;            // max_initial_timestamp_index, < 0: none
   float scale;                 // logit dequantisation scale (> 0)
+  float *sum_logprobs;         // per row, or null: += log_softmax of the filtered logits at the token
+  int32_t *eot_count;          // [hist_cols], or null: rows whose new token is EOT, per step
 };
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -613,8 +615,8 @@ __global__ __launch_bounds__(256) void greedy_filtered_kernel(const int8_t *__re
                                                               int64_t hist_cols, const int32_t *step,
                                                               GreedyFilter f) {
   __shared__ uint32_t s_kt[4], s_ks[4];
-  __shared__ int32_t s_m[4], s_i[4];
-  __shared__ float s_s[4];
+  __shared__ int32_t s_m[4], s_i[4], s_mx[4];
+  __shared__ float s_s[4], s_sx[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
   const int n = (int)cols;
@@ -658,10 +660,12 @@ __global__ __launch_bounds__(256) void greedy_filtered_kernel(const int8_t *__re
   const uint32_t *mk = (st == 0 && f.mask_first) ? f.mask_first : f.mask;
   const int nw = (n + 31) >> 5;
 
-  // ---- one pass: text argmax key, timestamp argmax key, timestamp (max, sum exp) ----
+  // ---- one pass: text argmax key, timestamp argmax key, timestamp (max, sum exp),
+  // and with sum_logprobs the text tokens' (max, sum exp) ----
+  const bool lps = f.sum_logprobs != nullptr;
   uint32_t kt = 0, ks = 0;
-  int32_t m = -1000;
-  float sum = 0.f;
+  int32_t m = -1000, mx = -1000;
+  float sum = 0.f, sumx = 0.f;
   const int8_t *xr = x + row * ld;
   for (int i0 = tid * 16; i0 < n; i0 += 256 * 16) {
     uint32_t bits = 0;
@@ -679,6 +683,14 @@ __global__ __launch_bounds__(256) void greedy_filtered_kernel(const int8_t *__re
       const uint32_t key = ((uint32_t)(v + 129) << 23) | (uint32_t)(0x7FFFFF - i);
       if (i >= text_lo && i < ts_b) {
         kt = max(kt, key);
+        if (lps) {
+          if (v > mx) {
+            sumx = sumx * expf((float)(mx - v) * f.scale) + 1.f;
+            mx = v;
+          } else {
+            sumx += expf((float)(v - mx) * f.scale);
+          }
+        }
       } else if (i >= ts_lo && i < ts_hi) {
         ks = max(ks, key);
         if (v > m) {
@@ -697,27 +709,207 @@ __global__ __launch_bounds__(256) void greedy_filtered_kernel(const int8_t *__re
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) sw += __shfl_xor(sw, o);
   if (lane == 0) s_kt[wave] = kt, s_ks[wave] = ks, s_m[wave] = mw, s_s[wave] = sw;
+  if (lps) {
+    const int32_t mxw = wave_max_i32(mx);
+    float sxw = sumx * expf((float)(mx - mxw) * f.scale);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sxw += __shfl_xor(sxw, o);
+    if (lane == 0) s_mx[wave] = mxw, s_sx[wave] = sxw;
+  }
   __syncthreads();
   if (tid == 0) {
     kt = max(max(s_kt[0], s_kt[1]), max(s_kt[2], s_kt[3]));
     ks = max(max(s_ks[0], s_ks[1]), max(s_ks[2], s_ks[3]));
     uint32_t key = max(kt, ks);
+    // the timestamps' (max, sum exp) over the allowed timestamps
+    const int32_t mt = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
+    float st_sum = 0.f;
+    for (int w = 0; w < 4; ++w) st_sum += s_s[w] * expf((float)(s_m[w] - mt) * f.scale);
+    bool ts_wins = false;
     if (rules && ks != 0) {
-      const int32_t mt = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
-      float st_sum = 0.f;
-      for (int w = 0; w < 4; ++w) st_sum += s_s[w] * expf((float)(s_m[w] - mt) * f.scale);
       const float lse_ts = (float)mt * f.scale + logf(st_sum);
-      const bool ts_wins = kt == 0 || lse_ts > (float)((int32_t)(kt >> 23) - 129) * f.scale;
+      ts_wins = kt == 0 || lse_ts > (float)((int32_t)(kt >> 23) - 129) * f.scale;
       if (ts_wins) key = ks;
     }
     int64_t idx = key == 0 ? 0 : (int64_t)(0x7FFFFF - (key & 0x7FFFFF));
+    bool after_eot = false;
     if (f.eot >= 0) {
       const int64_t prev = nh >= 1 ? h[nh - 1] : (f.prev0 ? f.prev0[row] : -1);
-      if (prev == f.eot) idx = f.eot;
+      after_eot = prev == f.eot;
     }
+    if (lps) {
+      // log_softmax of the filtered logits at the chosen token: the chosen
+      // value is the maximum of the allowed set, which is the timestamps alone
+      // when they win (the text logits are then -inf) and text + timestamps
+      // otherwise; nothing allowed gives NaN, as log_softmax over all -inf
+      float lp;
+      if (key == 0) {
+        lp = __builtin_nanf("");
+      } else if (ts_wins || kt == 0) {
+        lp = -logf(st_sum);
+      } else {
+        const int32_t mxt = max(max(s_mx[0], s_mx[1]), max(s_mx[2], s_mx[3]));
+        float sx = 0.f;
+        for (int w = 0; w < 4; ++w) sx += s_sx[w] * expf((float)(s_mx[w] - mxt) * f.scale);
+        const int32_t top = (int32_t)(key >> 23) - 129;  // the chosen value
+        float total = sx * expf((float)(mxt - top) * f.scale);
+        if (ks != 0) total += st_sum * expf((float)(mt - top) * f.scale);
+        lp = -logf(total);
+      }
+      // the reference adds lp * (previous token != EOT)
+      f.sum_logprobs[row] += after_eot ? lp * 0.f : lp;
+    }
+    if (after_eot) idx = f.eot;
     out[row] = idx;
-    if (st >= 0 && st < hist_cols) history[row * hist_ld + st] = idx;
+    if (st >= 0 && st < hist_cols) {
+      history[row * hist_ld + st] = idx;
+      if (f.eot_count && f.eot >= 0 && idx == f.eot) atomicAdd(f.eot_count + st, 1);
+    }
   }
+}
+
+// The sum of e[x + 128] over the int8 values x of one row (256 threads, the
+// row read in 16-byte pieces from its first 16-byte boundary), in float32.
+__device__ __forceinline__ float row_table_sum(const int8_t *xr, int n, const float *e) {
+  const int tid = threadIdx.x;
+  const int head = min((int)((16 - (reinterpret_cast<uintptr_t>(xr) & 15)) & 15), n);
+  const int pieces = (n - head) >> 4;
+  const int tail0 = head + (pieces << 4);
+  float s = 0.f;
+  if (tid < head) s += e[xr[tid] + 128];
+  const uint4 *xa = reinterpret_cast<const uint4 *>(xr + head);
+  for (int c = tid; c < pieces; c += 256) {
+    const uint4 w = xa[c];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 16; ++q) s += e[(int32_t)(int8_t)(ws[q >> 2] >> (8 * (q & 3))) + 128];
+  }
+  if (tail0 + tid < n) s += e[xr[tail0 + tid] + 128];
+  return s;
+}
+
+__device__ __forceinline__ float block_sum_f32(float v, float *sh) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & 63) == 0) sh[tid >> 6] = v;
+  __syncthreads();
+  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+
+// One step of GreedyDecoder.update (decoding.py:280-296) at temperature 0,
+// one block per row:
+//  * next token = first index of the row maximum of the int8 logits, from the
+//    classifier's per-32-column-tile maxima (amax, tiles per row) or, without
+//    them, from the logits row itself;
+//  * sum_logprobs[row] += log_softmax(logits * scale)[next], added only when
+//    the previous token is not EOT (:287-289): for the row maximum v that is
+//    -log(sum_i exp((x_i - v) * scale)), the sum taken through a 256-entry
+//    table of exp((x - v) * scale) over the int8 values x;
+//  * a row whose previous token is EOT emits EOT (:291); the number of rows
+//    whose new token is EOT is added to eot_count[*step] (completed = that
+//    count equals the batch, :293);
+//  * history[row][*step] = next_tokens[row] = the token; then the last block to
+//    finish advances *step by 1 and *pos by pos_inc (every block has read
+//    *step by then: each one's arrival on `arrive` comes after its read).
+struct GreedyUpdate {
+  const uint16_t *amax = nullptr;
+  int64_t tiles = 0;
+  const int8_t *logits = nullptr;
+  int64_t ld = 0;
+  int cols = 0;
+  int64_t *next = nullptr;
+  int64_t *history = nullptr;
+  int64_t hist_ld = 0, hist_cols = 0;
+  int32_t *step = nullptr, *pos = nullptr;
+  int32_t pos_inc = 0;
+  int32_t eot = -1;
+  const int64_t *prev0 = nullptr;
+  float *sum_logprobs = nullptr;
+  float scale = 1.f;
+  int32_t *eot_count = nullptr;
+  uint32_t *arrive = nullptr;
+};
+
+__global__ __launch_bounds__(256) void greedy_update_kernel(GreedyUpdate p) {
+  __shared__ int32_t s_st;
+  __shared__ uint32_t s_k[4];
+  __shared__ float s_f[4];
+  __shared__ float s_e[256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  if (tid == 0) s_st = *p.step;
+  // first maximum: key (v + 128) << 23 | (2^23 - 1 - index)
+  uint32_t key = 0;
+  if (p.amax) {
+    const uint16_t *ar = p.amax + row * p.tiles;
+    for (int64_t t = tid; t < p.tiles; t += 256) {
+      const uint32_t q = ar[t];
+      if (q) {
+        const uint32_t i = (uint32_t)t * 32u + (31u - (q & 31u));
+        key = max(key, ((q >> 5) << 23) | (0x7FFFFFu - i));
+      }
+    }
+  } else {
+    const int8_t *xr = p.logits + row * p.ld;
+    for (int i = tid; i < p.cols; i += 256)
+      key = max(key, ((uint32_t)(xr[i] + 128) << 23) | (uint32_t)(0x7FFFFF - i));
+  }
+  key = wave_max_u32(key);
+  if (lane == 0) s_k[wave] = key;
+  __syncthreads();  // s_st, s_k
+  key = max(max(s_k[0], s_k[1]), max(s_k[2], s_k[3]));
+  const int st = s_st;
+  const int32_t vmax = (int32_t)(key >> 23) - 128;
+  const int64_t idx = (int64_t)(0x7FFFFF - (key & 0x7FFFFF));
+  float lp = 0.f;
+  if (p.sum_logprobs) {
+    s_e[tid] = expf((float)(tid - 128 - vmax) * p.scale);
+    __syncthreads();
+    lp = -logf(block_sum_f32(row_table_sum(p.logits + row * p.ld, p.cols, s_e), s_f));
+  }
+  if (tid == 0) {
+    const int64_t prev = st >= 1 ? (st - 1 < p.hist_cols ? p.history[row * p.hist_ld + st - 1] : -1)
+                                 : (p.prev0 ? p.prev0[row] : -1);
+    const bool after_eot = p.eot >= 0 && prev == p.eot;
+    const int64_t tok = after_eot ? p.eot : idx;
+    p.next[row] = tok;
+    if (st >= 0 && st < p.hist_cols) {
+      p.history[row * p.hist_ld + st] = tok;
+      if (p.eot_count && p.eot >= 0 && tok == p.eot) atomicAdd(p.eot_count + st, 1);
+    }
+    // the reference adds lp * (previous token != EOT)
+    if (p.sum_logprobs) p.sum_logprobs[row] += after_eot ? lp * 0.f : lp;
+    // this block has read *step (s_st, above a barrier): arrive
+    if (atomicAdd(p.arrive, 1u) == gridDim.x - 1) {
+      *p.step = st + 1;
+      *p.pos += p.pos_inc;
+      *p.arrive = 0;
+    }
+  }
+}
+
+// softmax(logits * scale)[token] of each row in float32 (the no-speech
+// probability at the start-of-transcript position, decoding.py:690-695):
+// exp((x_token - v) * scale) / sum_i exp((x_i - v) * scale), v the row maximum.
+__global__ __launch_bounds__(256) void token_prob_kernel(const int8_t *__restrict__ x, int64_t ld, int cols,
+                                                         int64_t token, float scale, float *__restrict__ out) {
+  __shared__ int32_t s_m[4];
+  __shared__ float s_f[4];
+  __shared__ float s_e[256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int8_t *xr = x + blockIdx.x * ld;
+  int32_t m = -128;
+  for (int i = tid; i < cols; i += 256) m = max(m, (int32_t)xr[i]);
+  m = wave_max_i32(m);
+  if (lane == 0) s_m[wave] = m;
+  __syncthreads();
+  m = max(max(s_m[0], s_m[1]), max(s_m[2], s_m[3]));
+  s_e[tid] = expf((float)(tid - 128 - m) * scale);
+  __syncthreads();
+  const float sum = block_sum_f32(row_table_sum(xr, cols, s_e), s_f);
+  if (tid == 0) out[blockIdx.x] = s_e[xr[token] + 128] / sum;
 }
 
 // Greedy step bookkeeping after argmax_rows wrote next[]: record the tokens
@@ -1005,9 +1197,9 @@ int launch_greedy_step_filtered(const int8_t *logits, int64_t rows, int64_t cols
                                 int64_t *history, int64_t hist_ld, int64_t hist_cols, int32_t *step,
                                 int32_t *pos, int32_t pos_inc, const uint32_t *mask, const uint32_t *mask_first,
                                 const int64_t *prev0, int32_t eot, int32_t ts_begin, int32_t max_init,
-                                float scale, hipStream_t s) {
+                                float scale, float *sum_logprobs, int32_t *eot_count, hipStream_t s) {
   if (rows > 0) {
-    const GreedyFilter f{mask, mask_first, prev0, eot, ts_begin, max_init, scale};
+    const GreedyFilter f{mask, mask_first, prev0, eot, ts_begin, max_init, scale, sum_logprobs, eot_count};
     hipLaunchKernelGGL(greedy_filtered_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, cols, ld, next,
                        history, hist_ld, hist_cols, step, f);
     int rc = check_launch("greedy_filtered_kernel");
@@ -1015,6 +1207,41 @@ int launch_greedy_step_filtered(const int8_t *logits, int64_t rows, int64_t cols
   }
   hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(64), 0, s, step, pos, pos_inc);
   return check_launch("greedy_advance_kernel");
+}
+
+int launch_greedy_update(const uint16_t *amax, int64_t tiles, const int8_t *logits, int64_t ld, int64_t rows,
+                         int64_t cols, int64_t *next, int64_t *history, int64_t hist_ld, int64_t hist_cols,
+                         int32_t *step, int32_t *pos, int32_t pos_inc, int32_t eot, const int64_t *prev0,
+                         float *sum_logprobs, float scale, int32_t *eot_count, uint32_t *arrive, hipStream_t s) {
+  GreedyUpdate p;
+  p.amax = amax;
+  p.tiles = tiles;
+  p.logits = logits;
+  p.ld = ld;
+  p.cols = (int)cols;
+  p.next = next;
+  p.history = history;
+  p.hist_ld = hist_ld;
+  p.hist_cols = hist_cols;
+  p.step = step;
+  p.pos = pos;
+  p.pos_inc = pos_inc;
+  p.eot = eot;
+  p.prev0 = prev0;
+  p.sum_logprobs = sum_logprobs;
+  p.scale = scale;
+  p.eot_count = eot_count;
+  p.arrive = arrive;
+  hipLaunchKernelGGL(greedy_update_kernel, dim3((unsigned)rows), dim3(256), 0, s, p);
+  return check_launch("greedy_update_kernel");
+}
+
+int launch_token_prob(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t token, float scale,
+                      float *out, hipStream_t s) {
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(token_prob_kernel, dim3((unsigned)rows), dim3(256), 0, s, logits, ld, (int)cols, token, scale,
+                     out);
+  return check_launch("token_prob_kernel");
 }
 
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,

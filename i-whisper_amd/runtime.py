@@ -288,7 +288,15 @@ class DecoderRunner:
 
     def __init__(self, decoder: TextDecoder_int, batch: int, n_audio_ctx: int,
                  max_steps: Optional[int] = None, use_graph: bool = True,
-                 filters: Optional[LogitFilters] = None, frag: bool = True, prefetch: bool = True):
+                 filters: Optional[LogitFilters] = None, frag: bool = True, prefetch: bool = True,
+                 eot: Optional[int] = None, logprobs: bool = True, no_speech: Optional[int] = None,
+                 sot_index: int = 0):
+        """``eot``: the EOT id for GreedyDecoder.update's EOT freeze and the
+        all-finished count without filters (the filters carry their own);
+        ``logprobs``: accumulate each row's sum of log-probabilities
+        (``sum_logprobs``); ``no_speech``: the no-speech token id, whose
+        probability at the prompt position ``sot_index`` the prompt step
+        records (``no_speech_probs``)."""
         self.dec = decoder
         self.B = batch
         C, H = decoder.n_state, decoder.n_head
@@ -343,6 +351,25 @@ class DecoderRunner:
         self.graph_multi = None  # GRAPH_STEPS steps in one graph
         self.graph_stream = None
         self.prev0 = torch.zeros(batch, dtype=torch.int64, device=dev)  # the prompt's last token
+        # GreedyDecoder.update's bookkeeping on the device: the per-tile row
+        # maxima of the fused classifier, the rows' log-probability sums, the
+        # number of rows whose token is EOT at each step, the arrival counter
+        # of the update kernel's blocks (0 between launches)
+        V = decoder.n_vocab
+        self.tiles = (V + 31) // 32
+        self.row_max = torch.zeros((batch, self.tiles), dtype=torch.uint16, device=dev)
+        self.eot = filters.eot if filters is not None else (-1 if eot is None else int(eot))
+        if filters is not None and eot is not None and int(eot) != filters.eot:
+            raise ValueError("eot differs from the filters' EOT id")
+        self.logprobs = logprobs
+        self.sum_logprobs = torch.zeros(batch, dtype=torch.float32, device=dev)
+        self.eot_count = torch.zeros(self.hist_cols, dtype=torch.int32, device=dev)
+        self.arrive = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.no_speech = no_speech
+        self.sot_index = sot_index
+        self.no_speech_probs = torch.full((batch,), float("nan"), dtype=torch.float32, device=dev)
+        self.steps_done = 0
+        self.logit_scale = 1.0 / float(decoder.act_logits_alpha.detach().reshape(-1)[0].item())
         self.filters = filters
         if filters is not None:
             V = decoder.n_vocab
@@ -381,6 +408,9 @@ class DecoderRunner:
     def reset(self):
         self.pos.zero_()
         self.step_no.zero_()
+        self.sum_logprobs.zero_()
+        self.eot_count.zero_()
+        self.no_speech_probs.fill_(float("nan"))
 
     # ---- shared pieces ----
     def _cross_attend(self, att, l, q_ptr, q_sb, q_st, Tq, out, table):
@@ -410,29 +440,42 @@ class DecoderRunner:
         self._cross_attend(att, layer, q.data_ptr(), self.C, self.C, 1, out, None)
 
     def _finish(self, x_last: torch.Tensor, pos_inc: int):
-        """Final LayerNorm of the last position, classifier, argmax, record, advance."""
+        """Final LayerNorm of the last position, classifier (with the row maxima
+        fused into its epilogue on the fragment-major path), then one
+        GreedyDecoder.update: token, EOT freeze, log-probability sum, EOT count,
+        history, counters."""
         dec = self.dec
         sc = dec.scalars()
+        f = self.filters
+        fused = self.frag and f is None
         if self.frag:
             _ln_frag(dec.ln, x_last, self.B, self.h8f)
-            _lib.call("iw_classifier_frag", self.h8f.data_ptr(), self.f_emb.data_ptr(), sc["cm"], sc["cs"],
-                      self.logits.data_ptr(), self.B, self.C, dec.n_vocab, _stream())
+            if fused:
+                _lib.call("iw_classifier_argmax_frag", self.h8f.data_ptr(), self.f_emb.data_ptr(), sc["cm"],
+                          sc["cs"], self.logits.data_ptr(), self.row_max.data_ptr(), self.B, self.C,
+                          dec.n_vocab, _stream())
+            else:
+                _lib.call("iw_classifier_frag", self.h8f.data_ptr(), self.f_emb.data_ptr(), sc["cm"], sc["cs"],
+                          self.logits.data_ptr(), self.B, self.C, dec.n_vocab, _stream())
         else:
             _ln(dec.ln, x_last, self.B, self.h8)
             _lib.call("iw_classifier", self.h8.data_ptr(), dec.token_embedding.weight.data_ptr(),
                       sc["cm"], sc["cs"], self.logits.data_ptr(), self.B, self.C, dec.n_vocab,
                       _stream())
-        f = self.filters
+        lp = self.sum_logprobs.data_ptr() if self.logprobs else None
         if f is None:
-            _lib.call("iw_greedy_advance", self.logits.data_ptr(), self.B, dec.n_vocab, dec.n_vocab,
-                      self.tokens.data_ptr(), self.history.data_ptr(), self.hist_cols, self.hist_cols,
-                      self.step_no.data_ptr(), self.pos.data_ptr(), pos_inc, _stream())
+            _lib.call("iw_greedy_update", self.row_max.data_ptr() if fused else None, self.tiles,
+                      self.logits.data_ptr(), dec.n_vocab, self.B, dec.n_vocab, self.tokens.data_ptr(),
+                      self.history.data_ptr(), self.hist_cols, self.hist_cols, self.step_no.data_ptr(),
+                      self.pos.data_ptr(), pos_inc, self.eot, self.prev0.data_ptr(), lp, self.logit_scale,
+                      self.eot_count.data_ptr() if self.eot >= 0 else None, self.arrive.data_ptr(), _stream())
         else:
             _lib.call("iw_greedy_advance_filtered", self.logits.data_ptr(), self.B, dec.n_vocab,
                       dec.n_vocab, self.tokens.data_ptr(), self.history.data_ptr(), self.hist_cols,
                       self.hist_cols, self.step_no.data_ptr(), self.pos.data_ptr(), pos_inc,
                       _ptr(self.f_mask), _ptr(self.f_first), self.prev0.data_ptr(), f.eot,
-                      f.timestamp_begin, f.max_initial_timestamp_index, self.f_scale, _stream())
+                      f.timestamp_begin, f.max_initial_timestamp_index, self.f_scale, lp,
+                      self.eot_count.data_ptr(), _stream())
 
     # ---- the prompt (several tokens, cache empty) ----
     def prompt_step(self, tokens: torch.Tensor):
@@ -441,6 +484,8 @@ class DecoderRunner:
         P = tokens.shape[1]
         if P > self.Tcap:
             raise ValueError("prompt longer than n_text_ctx")
+        if self.no_speech is not None and not 0 <= self.sot_index < P:
+            raise ValueError("sot_index outside the prompt")
         M = B * P
         dev = tokens.device
         x16 = dec.embed(tokens.view(B, P), 0).view(M, C)
@@ -473,6 +518,18 @@ class DecoderRunner:
             _ln(blk.mlp_ln, x16, M, h8)
             _mlp_gelu(blk, h8.data_ptr(), M, f8)
             _lin32_res(blk.mlp[2], f8.data_ptr(), M, x16, sc["m"])
+        if self.no_speech is not None:
+            # the no-speech probability at the start-of-transcript position
+            # (decoding.py:690-695): softmax of that position's logits
+            sot = x16.view(B, P, C)[:, self.sot_index].contiguous()
+            h = torch.empty((B, C), dtype=torch.int8, device=dev)
+            lg = torch.empty((B, dec.n_vocab), dtype=torch.int8, device=dev)
+            _ln(dec.ln, sot, B, h)
+            sc0 = dec.scalars()
+            _lib.call("iw_classifier", h.data_ptr(), dec.token_embedding.weight.data_ptr(), sc0["cm"], sc0["cs"],
+                      lg.data_ptr(), B, C, dec.n_vocab, _stream())
+            _lib.call("iw_token_prob", lg.data_ptr(), B, dec.n_vocab, dec.n_vocab, self.no_speech,
+                      self.logit_scale, self.no_speech_probs.data_ptr(), _stream())
         last = x16.view(B, P, C)[:, P - 1].contiguous()
         self._finish(last, P)
 
@@ -592,8 +649,12 @@ class DecoderRunner:
         for _ in range(n):
             self.graph.replay()
 
-    def run(self, prompt: torch.Tensor, steps: int, keep_logits: bool = False):
-        """Greedy tokens [B, steps] after ``prompt`` (and the int8 logits of every step)."""
+    def run(self, prompt: torch.Tensor, steps: int, keep_logits: bool = False, stop_on_eot: bool = False):
+        """Greedy tokens [B, steps] after ``prompt`` (and the int8 logits of every step).
+        With ``stop_on_eot`` (needs an EOT id) decoding ends once every row's
+        latest token is EOT (DecodingTask._main_loop's ``completed``,
+        decoding.py:710), checked after each graph replay; the tokens then end
+        at that step. ``steps_done`` holds the number of steps taken."""
         if prompt.dim() != 2 or prompt.shape[0] != self.B or prompt.shape[1] < 1:
             raise ValueError(f"prompt of shape {tuple(prompt.shape)}; this runner takes [{self.B}, P >= 1]")
         if prompt.dtype != torch.int64 or not prompt.is_cuda:
@@ -604,21 +665,41 @@ class DecoderRunner:
             raise ValueError(f"prompt + steps exceeds n_text_ctx ({self.Tcap})")
         if steps > self.hist_cols:
             raise ValueError("more steps than the history holds")
+        if stop_on_eot and self.eot < 0:
+            raise ValueError("stop_on_eot needs the EOT id (eot= or filters)")
         self.reset()
         self.prev0.copy_(prompt[:, -1])
         logits = []
         self.prompt_step(prompt.contiguous())
+        done = 1
         if keep_logits:
             logits.append(self.logits.clone())
-            for _ in range(steps - 1):
+            while done < steps and not (stop_on_eot and self._all_eot(done)):
                 self.decode_step()
                 logits.append(self.logits.clone())
-        else:
+                done += 1
+        elif not stop_on_eot:
             self._replay(steps - 1)
-        toks = self.history[:, :steps]
+            done = steps
+        else:
+            while done < steps and not self._all_eot(done):
+                n = min(self.GRAPH_STEPS, steps - done)
+                self._replay(n)
+                done += n
+            # the replays past the finishing step only repeat EOT; end at it
+            cnt = self.eot_count[:done].cpu()
+            fin = (cnt == self.B).nonzero()
+            if len(fin):
+                done = int(fin[0]) + 1
+        self.steps_done = done
+        toks = self.history[:, :done]
         if keep_logits:
             return toks, torch.stack(logits, 1)
         return toks
+
+    def _all_eot(self, done: int) -> bool:
+        """Whether every row's token of step ``done - 1`` is EOT (one read of the device count)."""
+        return int(self.eot_count[done - 1]) == self.B
 
     def run_forced(self, prompt: torch.Tensor, forced: torch.Tensor):
         """Teacher-forced steps: the prompt step, then one step per column of
@@ -643,13 +724,30 @@ class DecoderRunner:
         return self.history[:, :n + 1].clone(), torch.stack(logits, 1)
 
 
+@dataclass
+class GreedyResult:
+    """What DecodingTask._main_loop returns for greedy decoding
+    (decoding.py:684-712): the tokens, each row's sum of log-probabilities of
+    its sampled tokens (up to its EOT) and the no-speech probability at the
+    start-of-transcript position (NaN without a no-speech id)."""
+    tokens: torch.Tensor           # int64 [B, prompt_len + steps]
+    sum_logprobs: torch.Tensor     # float32 [B]
+    no_speech_probs: torch.Tensor  # float32 [B]
+    steps: int                     # greedy steps taken (fewer than asked when all rows ended)
+
+
 def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torch.Tensor,
                   steps: int, runner: Optional[DecoderRunner] = None,
-                  keep_logits: bool = False, filters: Optional[LogitFilters] = None):
-    """Fixed-step greedy decoding; returns int64 tokens [B, prompt_len + steps] (and the int8
-    logits of every step [B, steps, vocab] when ``keep_logits``). With ``filters`` the decoding
-    task's logit filters and the EOT freeze apply at every step on the device; without them the
-    choice is the plain first-index argmax."""
+                  keep_logits: bool = False, filters: Optional[LogitFilters] = None,
+                  eot: Optional[int] = None, no_speech: Optional[int] = None, stop_on_eot: bool = False,
+                  return_result: bool = False):
+    """Greedy decoding; returns int64 tokens [B, prompt_len + steps] (and the int8 logits of
+    every step [B, steps, vocab] when ``keep_logits``), or a GreedyResult with
+    ``return_result``. With ``filters`` the decoding task's logit filters and the EOT freeze
+    apply at every step on the device; without them the choice is the plain first-index argmax
+    (with the EOT freeze when ``eot`` is given). ``stop_on_eot`` ends decoding once every row
+    has emitted EOT. A given ``runner`` must have been built with the same filters, EOT and
+    no-speech ids."""
     B, P = prompt.shape
     dec = model.decoder
     if P + steps > dec.n_ctx:
@@ -660,13 +758,20 @@ def greedy_decode(model: Whisper_int, audio_features: torch.Tensor, prompt: torc
         return prompt.clone()
     if runner is None:
         runner = DecoderRunner(dec, B, audio_features.shape[1], use_graph=not keep_logits,
-                               filters=filters)
-    elif runner.filters is not filters:
-        raise ValueError("the runner was built with other logit filters (pass the runner's own "
-                         "filters, or None for a runner built without filters)")
+                               filters=filters, eot=eot, no_speech=no_speech)
+    else:
+        if runner.filters is not filters:
+            raise ValueError("the runner was built with other logit filters (pass the runner's own "
+                             "filters, or None for a runner built without filters)")
+        if (eot is not None and int(eot) != runner.eot) or (no_speech is not None and no_speech != runner.no_speech):
+            raise ValueError("the runner was built with another EOT or no-speech id")
     runner.set_audio(audio_features)
-    res = runner.run(prompt, steps, keep_logits=keep_logits)
+    res = runner.run(prompt, steps, keep_logits=keep_logits, stop_on_eot=stop_on_eot)
+    logits = None
     if keep_logits:
-        toks, logits = res
-        return torch.cat([prompt, toks], 1), logits
-    return torch.cat([prompt, res], 1)
+        res, logits = res
+    toks = torch.cat([prompt, res], 1)
+    if return_result:
+        out = GreedyResult(toks, runner.sum_logprobs.clone(), runner.no_speech_probs.clone(), runner.steps_done)
+        return (out, logits) if keep_logits else out
+    return (toks, logits) if keep_logits else toks

@@ -310,6 +310,13 @@ int iw_greedy_advance(const int8_t *logits, int64_t rows, int64_t cols, int64_t 
  *   logit_scale     the logits' dequantisation scale (> 0), for the rule that
  *                   compares logsumexp over timestamps with the best text
  *                   logit in fp32
+ *   sum_logprobs    [rows] float32 or NULL: += log_softmax of the filtered,
+ *                   dequantised logits (x * logit_scale, suppressed = -inf)
+ *                   at the chosen token, unless the previous token is EOT
+ *                   (GreedyDecoder.update, decoding.py:287-289); NaN for an
+ *                   all-suppressed row
+ *   eot_count       [history_cols] int32 or NULL: eot_count[*step] += the
+ *                   number of rows whose new token is EOT
  * All-suppressed rows give token 0 (torch.argmax over -inf). Then as
  * iw_greedy_advance: history[r][*step] = next, *step += 1, *pos += pos_increment. */
 int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld,
@@ -318,7 +325,8 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
                                int32_t pos_increment, const uint32_t *suppress,
                                const uint32_t *suppress_first, const int64_t *prev0, int32_t eot,
                                int32_t timestamp_begin, int32_t max_initial_timestamp,
-                               float logit_scale, iw_stream_t stream);
+                               float logit_scale, float *sum_logprobs, int32_t *eot_count,
+                               iw_stream_t stream);
 
 /* -------------------------------------------------------------------------
  * Fragment-major operands of the one-token decode step. No counterpart in
@@ -398,6 +406,42 @@ int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *
  * row-major [M][N]. */
 int iw_classifier_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift,
                        int8_t *out, int64_t M, int64_t K, int64_t N, iw_stream_t stream);
+
+/* iw_classifier_frag with the greedy argmax fused into its epilogue (the
+ * classifier of model_int.py:1446-1484 followed by the argmax of
+ * GreedyDecoder.update, decoding.py:280-296): also writes, for each row m and
+ * each 32-column tile t, the first maximum of the int8 logits in the tile,
+ * row_max[m * ceil(N / 32) + t] = (y + 128) << 5 | (31 - column in tile).
+ * out may be NULL (no logits written). N < 2^23. */
+int iw_classifier_argmax_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier,
+                              int8_t shift, int8_t *out, uint16_t *row_max, int64_t M, int64_t K,
+                              int64_t N, iw_stream_t stream);
+
+/* One step of GreedyDecoder.update (decoding.py:280-296) at temperature 0
+ * for rows of int8 logits (dequantised by logit_scale > 0):
+ *   next token   the first index of the row maximum, from row_max (the
+ *                tile maxima of iw_classifier_argmax_frag, tiles = ceil(cols /
+ *                32)) or, when row_max is NULL, from logits [rows][ld];
+ *   EOT freeze   with eot >= 0, a row whose previous token (history[r][*step -
+ *                1], or prev0[r] at *step 0) is EOT emits EOT;
+ *   sum_logprobs [rows] or NULL: += log_softmax(logits * logit_scale) at the
+ *                token, unless the previous token is EOT (needs logits);
+ *   eot_count    [history_cols] or NULL: eot_count[*step] += rows whose new
+ *                token is EOT (all rows finished = the count equals rows);
+ * then history[r][*step] = next_tokens[r] = token, *step += 1, *pos +=
+ * pos_increment. arrive: one uint32 that is 0 between calls (the kernel's
+ * blocks count their arrival there; the last one resets it). */
+int iw_greedy_update(const uint16_t *row_max, int64_t tiles, const int8_t *logits, int64_t ld,
+                     int64_t rows, int64_t cols, int64_t *next_tokens, int64_t *history,
+                     int64_t history_ld, int64_t history_cols, int32_t *step, int32_t *pos,
+                     int32_t pos_increment, int32_t eot, const int64_t *prev0, float *sum_logprobs,
+                     float logit_scale, int32_t *eot_count, uint32_t *arrive, iw_stream_t stream);
+
+/* out[r] = softmax(logits[r] * logit_scale)[token] in float32: the no-speech
+ * probability at the start-of-transcript position (DecodingTask._main_loop,
+ * decoding.py:690-695). */
+int iw_token_prob(const int8_t *logits, int64_t rows, int64_t cols, int64_t ld, int64_t token,
+                  float logit_scale, float *out, iw_stream_t stream);
 
 /* Log-mel spectrogram (log_mel_spectrogram, audio.py:216-267, with N_FFT =
  * 512, HOP_LENGTH = 160): for each of `batch` rows of float32 audio

@@ -125,3 +125,26 @@ def timestamp_margin(logits: np.ndarray, tokens: np.ndarray, spec: FilterSpec) -
         if ts.size and tx.size:
             out[k] = abs(ts.max() + np.log(np.sum(np.exp(ts - ts.max()))) - tx.max())
     return out
+
+
+def greedy_update(logits: np.ndarray, tokens: np.ndarray, eot: int, sum_logprobs: np.ndarray):
+    """GreedyDecoder.update (decoding.py:279-296) at temperature 0 on float32
+    logits [B, V] that the filters have already masked: returns the next tokens
+    (EOT after EOT), the updated float32 sum of log-probabilities and whether
+    every row's new token is EOT."""
+    logits = np.asarray(logits, dtype=np.float32)
+    nxt = np.argmax(logits, axis=-1).astype(np.int64)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        current = _log_softmax(logits)[np.arange(logits.shape[0]), nxt]
+        keep = (tokens[:, -1] != eot).astype(np.float32)
+        sum_logprobs = (np.asarray(sum_logprobs, np.float32) + current * keep).astype(np.float32)
+    nxt[tokens[:, -1] == eot] = eot
+    return nxt, sum_logprobs, bool((nxt == eot).all())
+
+
+def token_prob(logits: np.ndarray, token: int) -> np.ndarray:
+    """softmax(logits.float())[:, token] (decoding.py:690-695), float32."""
+    x = np.asarray(logits, dtype=np.float32)
+    m = np.max(x, axis=-1, keepdims=True)
+    e = np.exp(x - m, dtype=np.float32)
+    return (e[:, token] / np.sum(e, axis=-1, dtype=np.float32)).astype(np.float32)

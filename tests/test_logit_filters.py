@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.logit_filters import FilterSpec, greedy_next, timestamp_margin
+from oracle.logit_filters import (FilterSpec, apply_filters, greedy_next, greedy_update, timestamp_margin,
+                                  token_prob)
 
 # toy vocabulary: text 0..5, EOT 6, <|notimestamps|> 7, timestamps 8..11
 TOY = FilterSpec(sample_begin=2, eot=6, suppress_tokens=[1], blank_ids=[0, 6], timestamp_begin=8,
@@ -154,7 +155,8 @@ def test_filtered_greedy_step_matches_oracle(iw, gpu, rules):
         spec = FilterSpec(sample_begin=3, eot=eot)
     B, hist_cols = 48, 40
     dev = "cuda"
-    always = sup + ([nots] if spec.timestamp_begin is not None else [])
+    # the device masks are exactly the spec's suppressions
+    always = list(spec.suppress_tokens) + ([nots] if spec.timestamp_begin is not None else [])
     m_all = torch.from_numpy(bitmask(always, V)).to(dev) if always else None
     m_first = torch.from_numpy(bitmask(always + (blank if spec.blank_ids else []), V)).to(dev)
     prompt = np.array([[50258, 50259, 50359]] * B, np.int64)
@@ -175,18 +177,30 @@ def test_filtered_greedy_step_matches_oracle(iw, gpu, rules):
         nxt = torch.empty(B, dtype=torch.int64, device=dev)
         step = torch.tensor([st], dtype=torch.int32, device=dev)
         pos = torch.tensor([3 + st], dtype=torch.int32, device=dev)
+        slp0 = rng.normal(-5, 2, B).astype(np.float32)
+        slp = torch.from_numpy(slp0.copy()).to(dev)
+        cnt = torch.zeros(hist_cols, dtype=torch.int32, device=dev)
         iw._lib.call("iw_greedy_advance_filtered", qt.data_ptr(), B, V, V, nxt.data_ptr(), ht.data_ptr(),
                      hist_cols, hist_cols, step.data_ptr(), pos.data_ptr(), 1,
                      m_all.data_ptr() if m_all is not None else None,
                      m_first.data_ptr() if spec.blank_ids else None, prev0.data_ptr(),
                      eot, spec.timestamp_begin if spec.timestamp_begin is not None else -1,
                      spec.max_initial_timestamp_index if spec.max_initial_timestamp_index is not None else -1,
-                     scale, torch.cuda.current_stream().cuda_stream)
+                     scale, slp.data_ptr(), cnt.data_ptr(), torch.cuda.current_stream().cuda_stream)
         got = nxt.cpu().numpy()
         assert np.array_equal(got[keep], want[keep]), (st, np.nonzero(got != want))
         assert np.array_equal(ht.cpu().numpy()[:, st], got)
         assert int(step.item()) == st + 1 and int(pos.item()) == 4 + st
         assert keep.mean() > 0.9
+        # GreedyDecoder.update's log-probability sum and the EOT count
+        w_next, w_slp, _ = greedy_update(apply_filters(f32, toks, spec), toks, eot, slp0)
+        assert np.array_equal(w_next[keep], got[keep])
+        g_slp = slp.cpu().numpy()
+        assert np.array_equal(np.isnan(g_slp[keep]), np.isnan(w_slp[keep]))
+        fin = keep & ~np.isnan(w_slp)
+        assert np.allclose(g_slp[fin], w_slp[fin], rtol=1e-5, atol=1e-4), (st, g_slp - w_slp)
+        c = cnt.cpu().numpy()
+        assert c[st] == int((got == eot).sum()) and c.sum() == c[st]
 
 
 @pytest.mark.gpu
@@ -221,3 +235,29 @@ def test_greedy_decode_with_filters(iw, gpu):
         assert np.array_equal(toks[keep, 3 + j], want[keep]), j
     # the first sampled token obeys the initial-timestamp rule
     assert ((toks[:, 3] >= tb) & (toks[:, 3] <= tb + 40)).all()
+
+
+def test_greedy_update_oracle_known_answers():
+    """GreedyDecoder.update's bookkeeping restated (decoding.py:279-296): the
+    log-probability of the argmax for uniform logits is -log(V), for two tied
+    maxima -log(2) (first index chosen), agrees with torch.log_softmax on random
+    rows, is not added after EOT, and the rows after EOT emit EOT."""
+    V, eot = 1000, 7
+    logits = np.zeros((4, V), np.float32)
+    logits[1, [3, 900]] = 50.0                      # two tied maxima, far above the rest
+    logits[2] = np.random.default_rng(1).normal(0, 3, V).astype(np.float32)
+    logits[3, eot] = 9.0
+    tokens = np.array([[1, 2], [1, 2], [1, 2], [1, eot]], np.int64)
+    nxt, slp, done = greedy_update(logits, tokens, eot, np.zeros(4, np.float32))
+    assert nxt.tolist()[:3] == [0, 3, int(np.argmax(logits[2]))] and nxt[3] == eot
+    assert np.isclose(slp[0], -np.log(V), atol=1e-5)
+    assert np.isclose(slp[1], -np.log(2), atol=1e-5)
+    want2 = torch.log_softmax(torch.from_numpy(logits[2]), -1)[nxt[2]].item()
+    assert np.isclose(slp[2], want2, atol=1e-5)
+    assert slp[3] == 0.0 and not done
+    _, _, done = greedy_update(logits[3:], tokens[3:], eot, np.zeros(1, np.float32))
+    assert done
+    # no-speech probability: softmax at a token
+    p = token_prob(logits, 3)
+    assert np.isclose(p[0], 1.0 / V) and np.isclose(p[1], 0.5, atol=1e-6)
+    assert np.isclose(p[2], torch.softmax(torch.from_numpy(logits[2]), -1)[3].item(), rtol=1e-5)
