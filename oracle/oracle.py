@@ -1,8 +1,11 @@
 """numpy front end of the CPU oracle (TEST INFRASTRUCTURE ONLY).
 
-Two libraries expose the same operations:
+Three libraries expose the same operations:
   * ``Oracle("oracle")`` - this repository's C restatement, oracle/iw_oracle.c
     (built by ``make -C oracle``), used on every machine;
+  * ``Oracle("simd")``   - the SIMD-shaped restatement, oracle/iw_cpu_simd.c
+    (dot-product tiles split over threads, as the reference's CPU backend
+    runs), bit-identical to the first; timed as bench.py's CPU baseline;
   * ``Oracle("ref")``    - the reference's own scalar kernels compiled from the
     reference tree behind oracle/ref_shim.cpp into oracle/_ref/ (``make -C
     oracle ref``); present only where that build was made.
@@ -22,6 +25,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIBS = {
     "oracle": HERE / "build" / "libiw_oracle.so",
+    "simd": HERE / "build" / "libiw_cpu_simd.so",
     "ref": HERE / "_ref" / "libiwref.so",
 }
 
@@ -55,8 +59,8 @@ class Oracle:
         if not path.exists():
             raise RuntimeError(f"{path} is not built")
         self.lib = C.CDLL(str(path))
-        self.pre = "iwo_" if kind == "oracle" else "ref_"
-        if kind == "oracle":
+        self.pre = {"oracle": "iwo_", "simd": "iws_"}.get(kind, "ref_")
+        if kind in ("oracle", "simd"):
             for fn, res in (("iwo_mulh", C.c_int32), ("iwo_rshift", C.c_int32),
                             ("iwo_requant", C.c_int32), ("iwo_fisr", C.c_int32),
                             ("iwo_shift_exp_one", C.c_uint8)):
@@ -71,7 +75,7 @@ class Oracle:
         return getattr(self.lib, self.pre + name)
 
     def _thr(self):
-        return (C.c_int(self.threads),) if self.kind == "oracle" else ()
+        return (C.c_int(self.threads),) if self.kind in ("oracle", "simd") else ()
 
     # ---- fixed point (oracle only) ----
     def mulh(self, x: int, m: int) -> int:
