@@ -136,24 +136,32 @@ def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: i
 
 
 PMC_SUMMARIES = (ROOT / "profiles" / "attn_decode_cross_b128_pmc.md",
-                 ROOT / "profiles" / "encoder_gemm_large_b128_pmc.md")
+                 ROOT / "profiles" / "encoder_gemm_large_b128_pmc.md",
+                 ROOT / "profiles" / "encoder_mfma_large_b128_pmc.md",
+                 ROOT / "profiles" / "large_b128_step_kernel_stats.md")
 GEMM_TRAFFIC_KEY = "gemm_dtl_kernel (encoder layer average)"
 # the decoder cross-attention kernel as profilers name it (key capacity, ring
 # slots, keys per chunk, waves per (batch, head))
 XA_KERNEL = "attn_decode_stream_kernel<2048, 3, 128, 4>"
 
 
-def recorded_traffic(kernel: str):
-    """HBM bytes per launch of ``kernel`` from the committed counter summaries
-    (a line ``traffic_bytes_per_launch <kernel>: <bytes>``), or None."""
+def recorded(key: str, kernel: str):
+    """A figure recorded in the committed profile summaries (a line
+    ``<key> <kernel>: <value>``), or None."""
     for path in PMC_SUMMARIES:
         try:
             for line in path.read_text().splitlines():
-                if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                if line.startswith(f"{key} {kernel}:"):
                     return float(line.rsplit(":", 1)[1])
         except OSError:
             pass
     return None
+
+
+def recorded_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed counter summaries
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy), or None."""
+    return recorded("traffic_bytes_per_launch", kernel)
 
 
 def cross_attention_probe(dec, dims, batch: int, launches: int = 20) -> float:
@@ -353,7 +361,15 @@ def main():
             "bound": "mfma", "kernel": "gemm_dtl_kernel (encoder QKV/out/FC1/FC2 launches)",
             "achieved": round(g_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
             "frac": round(g_tops / INT8_PEAK_TOPS, 4), "traffic": recorded_traffic(GEMM_TRAFFIC_KEY),
-            "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4)},
+            "ops_per_launch": g_ops, "avg_launch_ms": round(g_ms, 4),
+            # counters (profiles/encoder_mfma_large_b128_pmc.md): the fraction of the int8
+            # MFMA pipes' cycles at work, SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x cycles)
+            "mfma_busy_pmc": recorded("mfma_busy_pmc", GEMM_TRAFFIC_KEY)},
+        "encoder_attention": {
+            "kernel": "attn_prefill_kernel<2, false>", "achieved_tops": round(a_tops, 1),
+            "ops": "4*B*H*T^2*D (QK^T and P.V)",
+            "mfma_busy_pmc": recorded("mfma_busy_pmc", "attn_prefill_kernel"),
+            "valu_busy_pmc": recorded("valu_busy_pmc", "attn_prefill_kernel")},
         "hbm_kernels": rowops,
     }
     if dsteps:
@@ -369,6 +385,12 @@ def main():
             "frac": round(xa_gbs / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(kname),
             "bytes_per_launch": xa_bytes, "avg_launch_ms": round(xa_ms, 4),
             "launches_per_step": dsteps * dims.n_text_layer}
+        # the same kernel's average inside the replayed decode graphs, from the
+        # committed kernel trace (profiles/large_b128_step_kernel_stats.md)
+        tr_us = recorded("in_step_avg_us", kname)
+        if tr_us and shape == "large" and batch == 128:
+            result["roofline"]["avg_launch_ms_in_step_trace"] = round(tr_us / 1000.0, 5)
+            result["roofline"]["frac_in_step_trace"] = round(xa_bytes / (tr_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     del model, enc, dec
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
