@@ -19,6 +19,8 @@
 #include "iw_gemm.hpp"
 #include "iw_kernels.hpp"
 
+#include <type_traits>
+
 namespace iw {
 
 namespace {
@@ -311,67 +313,75 @@ void attn_prefill_kernel(AttnArgs a) {
         load_k(kc + 1);
         load_v(kc + 1);
       }
-      const bool full = !HAS_MASK && (kc + 1) * PF_KC <= a.Tk;
+      // A chunk of keys all below Tk and without a mask takes no per-key
+      // test; it is its own instance of the loop body (FULL), so that the
+      // compiler cannot merge the two and keep the tests on every score.
+      auto chunk = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const v16i s = scores(sub);
-        const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
-        // P of the 16 keys: requant (24-bit product: |score| < 2^21 and an
-        // 8-bit multiplier), round-half-away shift, int16 saturation, then
-        // the table at min((rowmax + 1 - h16) mod 2^16, size - 1)
-        // (keys past Tk or masked: P = 0, applied as a byte mask on the
-        // loaded value rather than a conditional write)
-        uint32_t pb[16];
+        for (int sub = 0; sub < 2; ++sub) {
+          const v16i s = scores(sub);
+          const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
+          // P of the 16 keys: requant (24-bit product: |score| < 2^21 and an
+          // 8-bit multiplier), round-half-away shift, int16 saturation, then
+          // the table at min((rowmax + 1 - h16) mod 2^16, size - 1)
+          // (keys past Tk or masked: P = 0, applied as a byte mask on the
+          // loaded value rather than a conditional write)
+          uint32_t pb[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          uint32_t keep = 0xffu;
-          if (!full) {
-            const int key = kbase0 + r;
-            bool ok = key < a.Tk;
-            if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
-            keep = ok ? 0xffu : 0u;
+          for (int r = 0; r < 16; ++r) {
+            const int32_t v = __mul24(s[r], qm24);
+            const uint32_t tr = (uint32_t)v + qhalf + (uint32_t)__builtin_amdgcn_sbfe(v, 31, qw);
+            const int32_t h16 = clampi((int32_t)tr >> qsh, -32768, 32767);
+            const uint32_t idx = min((rmp1 - (uint32_t)h16) & 0xffffu, (uint32_t)(IW_SEXP_LUT - 1));
+            pb[r] = (uint32_t)sLut[idx];
+            if constexpr (!FULL) {
+              const int key = kbase0 + r;
+              bool ok = key < a.Tk;
+              if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
+              pb[r] &= ok ? 0xffu : 0u;
+            }
           }
-          const int32_t v = __mul24(s[r], qm24);
-          const uint32_t tr = (uint32_t)v + qhalf + (uint32_t)__builtin_amdgcn_sbfe(v, 31, qw);
-          const int32_t h16 = clampi((int32_t)tr >> qsh, -32768, 32767);
-          const uint32_t idx = min((rmp1 - (uint32_t)h16) & 0xffffu, (uint32_t)(IW_SEXP_LUT - 1));
-          pb[r] = (uint32_t)sLut[idx] & keep;
-        }
-        uint32_t pw[4];
+          uint32_t pw[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          pw[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pb[4 * j + 3], pb[4 * j + 2], 0x0c0c0400u),
-                                        __builtin_amdgcn_perm(pb[4 * j + 1], pb[4 * j], 0x0c0c0400u),
-                                        0x05040100u);
-        const uint32_t ones = 0x01010101u;
-        psum = __builtin_amdgcn_udot4(pw[0], ones, psum, false);
-        psum = __builtin_amdgcn_udot4(pw[1], ones, psum, false);
-        psum = __builtin_amdgcn_udot4(pw[2], ones, psum, false);
-        psum = __builtin_amdgcn_udot4(pw[3], ones, psum, false);
-        // P <= 127 except at x_sub == 0 after an int16 row-max wrap (P = 128).
-        // int8 MFMA is signed, so such tiles split P = lo + 64 * hi2.
-        const uint32_t hib = (pw[0] | pw[1] | pw[2] | pw[3]) & 0x80808080u;
-        const bool any_hi = __any(hib != 0u);
-        v4i pa, ph;
-        if (!any_hi) {
-          pa = v4i{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
-        } else {
-          pa = v4i{(int)(pw[0] & 0x7f7f7f7fu), (int)(pw[1] & 0x7f7f7f7fu),
-                   (int)(pw[2] & 0x7f7f7f7fu), (int)(pw[3] & 0x7f7f7f7fu)};
-          ph = v4i{(int)((pw[0] >> 1) & 0x40404040u), (int)((pw[1] >> 1) & 0x40404040u),
-                   (int)((pw[2] >> 1) & 0x40404040u), (int)((pw[3] >> 1) & 0x40404040u)};
-        }
+          for (int j = 0; j < 4; ++j)
+            pw[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pb[4 * j + 3], pb[4 * j + 2], 0x0c0c0400u),
+                                          __builtin_amdgcn_perm(pb[4 * j + 1], pb[4 * j], 0x0c0c0400u),
+                                          0x05040100u);
+          const uint32_t ones = 0x01010101u;
+          psum = __builtin_amdgcn_udot4(pw[0], ones, psum, false);
+          psum = __builtin_amdgcn_udot4(pw[1], ones, psum, false);
+          psum = __builtin_amdgcn_udot4(pw[2], ones, psum, false);
+          psum = __builtin_amdgcn_udot4(pw[3], ones, psum, false);
+          // P <= 127 except at x_sub == 0 after an int16 row-max wrap (P = 128).
+          // int8 MFMA is signed, so such tiles split P = lo + 64 * hi2.
+          const uint32_t hib = (pw[0] | pw[1] | pw[2] | pw[3]) & 0x80808080u;
+          const bool any_hi = __any(hib != 0u);
+          v4i pa, ph;
+          if (!any_hi) {
+            pa = v4i{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
+          } else {
+            pa = v4i{(int)(pw[0] & 0x7f7f7f7fu), (int)(pw[1] & 0x7f7f7f7fu),
+                     (int)(pw[2] & 0x7f7f7f7fu), (int)(pw[3] & 0x7f7f7f7fu)};
+            ph = v4i{(int)((pw[0] >> 1) & 0x40404040u), (int)((pw[1] >> 1) & 0x40404040u),
+                     (int)((pw[2] >> 1) & 0x40404040u), (int)((pw[3] >> 1) & 0x40404040u)};
+          }
 #pragma unroll
-        for (int t = 0; t < KS; ++t) {
-          const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + sub * 32 + g * 16]);
-          o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, vb, o[t], 0, 0, 0);
-          if (any_hi) {
-            // 128 * hi = 64 * hi + 64 * hi
-            o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ph, vb, o[t], 0, 0, 0);
-            o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ph, vb, o[t], 0, 0, 0);
+          for (int t = 0; t < KS; ++t) {
+            const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + sub * 32 + g * 16]);
+            o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, vb, o[t], 0, 0, 0);
+            if (any_hi) {
+              // 128 * hi = 64 * hi + 64 * hi
+              o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ph, vb, o[t], 0, 0, 0);
+              o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ph, vb, o[t], 0, 0, 0);
+            }
           }
         }
-      }
+      };
+      if (!HAS_MASK && (kc + 1) * PF_KC <= a.Tk)
+        chunk(std::true_type{});
+      else
+        chunk(std::false_type{});
       __syncthreads();
     }
     psum += (uint32_t)__shfl_xor((int)psum, 32);
