@@ -89,8 +89,8 @@ def _timed_sample(iw, ref, dims, steps_total: int, enc_blocks: int, dec_steps: i
     return enc, dec, spent
 
 
-def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: int = 4,
-                 dec_steps: int = 6) -> dict:
+def cpu_baseline(iw, dims, params, steps_total: int, threads: int, enc_blocks: int = 8,
+                 dec_steps: int = 24) -> dict:
     """The reference's CPU algorithm timed on this host: the SIMD-shaped
     restatement (oracle/iw_cpu_simd.c: int8 dot-product tiles split over
     threads for the GEMM-shaped kernels, the row kernels and the classifier on
