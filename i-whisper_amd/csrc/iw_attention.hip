@@ -147,6 +147,14 @@ __global__ void shift_exp_lut_kernel(uint8_t *lut, int32_t f) {
 
 constexpr int PF_KC = 64;  // keys per LDS stage
 
+// Median of three signed ints: clamp of x to [lo, hi] for lo <= hi, in one
+// instruction where the bounds are not compile-time constants.
+__device__ __forceinline__ int32_t med3i(int32_t x, int32_t lo, int32_t hi) {
+  int32_t r;
+  asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+  return r;
+}
+
 __device__ __forceinline__ int key_row(int kk) {
   // LDS row of key kk (0..31) inside a 32-key sub-block
   const int g = kk >> 4, r = kk & 15;
@@ -175,7 +183,16 @@ void attn_prefill_kernel(AttnArgs a) {
   const int nkc = (a.Tk + PF_KC - 1) / PF_KC;
   const int D = a.D;
 
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  // Workgroup x runs on XCD x % 8 (round-robin dispatch). With a grid that
+  // is a multiple of 8, each XCD takes one contiguous range of tiles, so the
+  // query tiles of one (batch, head) share their K and V^T in that XCD's L2.
+  const int64_t G = gridDim.x;
+  const bool xcd_map = G % 8 == 0;
+  const int64_t per_xcd = xcd_map ? (ntiles + 7) / 8 : ntiles;
+  const int64_t t0 = xcd_map ? (int64_t)(blockIdx.x % 8) * per_xcd : 0;
+  const int64_t t1 = min(t0 + per_xcd, ntiles);
+  const int64_t tstep = xcd_map ? G / 8 : G;
+  for (int64_t tile = t0 + (xcd_map ? blockIdx.x / 8 : blockIdx.x); tile < t1; tile += tstep) {
     const int qt = (int)(tile % qtiles);
     const int64_t bh = tile / qtiles;
     const int h = (int)(bh % a.H);
@@ -256,9 +273,11 @@ void attn_prefill_kernel(AttnArgs a) {
     };
 
     // ---- pass 1: row max of the raw scores over unmasked keys ----
+    // The chunks whose keys are all below Tk (no mask) take no per-key test
+    // and run as a loop of their own, ahead of the rest.
     int32_t mx = INT32_MIN;
-    load_k(0);
-    for (int kc = 0; kc < nkc; ++kc) {
+    auto pass1 = [&](int kc, auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
       store_k();
       __syncthreads();
       // next: K chunk kc + 1, or pass 2's first K and V chunks
@@ -268,16 +287,20 @@ void attn_prefill_kernel(AttnArgs a) {
         load_k(0);
         load_v(0);
       }
-      // a chunk of keys all below Tk and no mask: no per-key test
-      const bool full = !HAS_MASK && (kc + 1) * PF_KC <= a.Tk;
+      // both sub-blocks' scores first: the second MFMA pair runs while the
+      // first sub-block's maximum is taken
+      v16i sc[2];
+      sc[0] = scores(0);
+      if constexpr (FULL) sc[1] = scores(1);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
-        const v16i s = scores(sub);
-        const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
-        if (full) {
+        if (!FULL && sub == 1) sc[1] = scores(1);
+        const v16i s = sc[sub];
+        if constexpr (FULL) {
 #pragma unroll
-          for (int r = 0; r < 16; r += 2) mx = max(mx, max(s[r], s[r + 1]));
+          for (int r = 0; r < 16; r += 2) mx = max(max(mx, s[r]), s[r + 1]);
         } else {
+          const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kbase0 + r;
@@ -288,7 +311,12 @@ void attn_prefill_kernel(AttnArgs a) {
         }
       }
       __syncthreads();
-    }
+    };
+    load_k(0);
+    const int nfull1 = HAS_MASK ? 0 : a.Tk / PF_KC;
+    int kc1 = 0;
+    for (; kc1 < nfull1; ++kc1) pass1(kc1, std::true_type{});
+    for (; kc1 < nkc; ++kc1) pass1(kc1, std::false_type{});
     mx = max(mx, __shfl_xor(mx, 32));
     const int32_t rowmax = mx == INT32_MIN ? -32768 : qk_requant16(mx, a.qk_m, a.qk_s);
     const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
@@ -299,13 +327,39 @@ void attn_prefill_kernel(AttnArgs a) {
     const uint32_t qsh = a.qk_s >= 32 ? 0u : a.qk_s;
     const uint32_t qhalf = qsh ? 1u << (qsh - 1) : 0u;
     const uint32_t qw = min(qsh, 1u);
+    // Keys of a full chunk all count in the row maximum, so with the row
+    // maximum below 32767 rowmax + 1 - h16 lies in [1, 65535] and the table
+    // index is
+    //   min(R - clamp16(h), L) = med3(R - h, min(R - 32767, L), min(R + 32768, L))
+    // with R = rowmax + 1 and h the unsaturated shift. R - h itself is one
+    // shift: with v = s * m, h = (v + half - [v < 0]) >> sh (floor), and
+    //   R - h = (R * 2^sh + 2^sh - 1 - half - v + [v < 0]) >> sh   (floor),
+    // which stays inside int32: |v| <= 2^21 * 255 < 2^29 and |R| <= 2^(29 - sh) + 2
+    // for sh <= 29. For sh >= 30 every h is 0 (|v| < 2^29 <= half), the same
+    // as m = 0 with sh = 0. [v < 0] = [s < 0] when m > 0; when m = 0 the term
+    // is below the rounding step either way (2^sh - half <= 2^sh - 1).
+    const uint32_t fsh = a.qk_s >= 30 ? 0u : a.qk_s;
+    const int32_t fnm = a.qk_s >= 30 ? 0 : -(int32_t)a.qk_m;
+    const uint32_t fw = min(fsh, 1u);
+    const int32_t fR = rowmax + 1;
+    const bool no_sat = !__any(rowmax >= 32767);
+    const int32_t fK = (int32_t)(((uint32_t)fR << fsh) + ((1u << fsh) - 1u) - (fsh ? 1u << (fsh - 1) : 0u));
+    const int32_t flo = min(fR - 32767, IW_SEXP_LUT - 1), fhi = min(fR + 32768, IW_SEXP_LUT - 1);
     v16i o[KS];
 #pragma unroll
     for (int t = 0; t < KS; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[t][r] = 0;
     uint32_t psum = 0;
-    for (int kc = 0; kc < nkc; ++kc) {
+    // Full chunks (all keys below Tk, no mask, no row maximum at 32767) run
+    // as a loop of their own with the short table index. There the index is
+    // at least 1, where the table holds at most 95 (x_sub <= -1 gives
+    // e < 0.75 * 2^f before the final shift to 7 fraction bits), so P fits
+    // the signed int8 MFMA operand as it is. The other chunks keep the
+    // per-key tests and the split of P = 128 (x_sub = 0 after the int16 wrap
+    // of a row maximum at 32767).
+    auto pass2 = [&](int kc, auto full_tag) {
+      constexpr bool FULL = decltype(full_tag)::value;
       store_k();
       store_v();
       __syncthreads();
@@ -313,54 +367,67 @@ void attn_prefill_kernel(AttnArgs a) {
         load_k(kc + 1);
         load_v(kc + 1);
       }
-      // A chunk of keys all below Tk and without a mask takes no per-key
-      // test; it is its own instance of the loop body (FULL), so that the
-      // compiler cannot merge the two and keep the tests on every score.
-      auto chunk = [&](auto full_tag) {
-        constexpr bool FULL = decltype(full_tag)::value;
+      // full chunks issue the second sub-block's score MFMAs ahead of the
+      // first sub-block's softmax, so they run under its VALU work
+      v16i sc[2];
+      sc[0] = scores(0);
+      if constexpr (FULL) sc[1] = scores(1);
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-          const v16i s = scores(sub);
-          const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
-          // P of the 16 keys: requant (24-bit product: |score| < 2^21 and an
-          // 8-bit multiplier), round-half-away shift, int16 saturation, then
-          // the table at min((rowmax + 1 - h16) mod 2^16, size - 1)
-          // (keys past Tk or masked: P = 0, applied as a byte mask on the
-          // loaded value rather than a conditional write)
-          uint32_t pb[16];
+      for (int sub = 0; sub < 2; ++sub) {
+        if (!FULL && sub == 1) sc[1] = scores(1);
+        const v16i s = sc[sub];
+        const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
+        // P of the 16 keys: requant (24-bit product: |score| < 2^21 and an
+        // 8-bit multiplier), round-half-away shift, int16 saturation, then
+        // the table at min((rowmax + 1 - h16) mod 2^16, size - 1)
+        // (keys past Tk or masked: P = 0, applied as a byte mask on the
+        // loaded value rather than a conditional write)
+        uint32_t pb[16];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < 16; ++r) {
+          uint32_t idx;
+          if constexpr (FULL) {
+            const uint32_t y = (uint32_t)(__mul24(s[r], fnm) + fK) -
+                               (uint32_t)__builtin_amdgcn_sbfe(s[r], 31, fw);
+            idx = (uint32_t)med3i((int32_t)y >> fsh, flo, fhi);
+          } else {
             const int32_t v = __mul24(s[r], qm24);
             const uint32_t tr = (uint32_t)v + qhalf + (uint32_t)__builtin_amdgcn_sbfe(v, 31, qw);
             const int32_t h16 = clampi((int32_t)tr >> qsh, -32768, 32767);
-            const uint32_t idx = min((rmp1 - (uint32_t)h16) & 0xffffu, (uint32_t)(IW_SEXP_LUT - 1));
-            pb[r] = (uint32_t)sLut[idx];
-            if constexpr (!FULL) {
-              const int key = kbase0 + r;
-              bool ok = key < a.Tk;
-              if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
-              pb[r] &= ok ? 0xffu : 0u;
-            }
+            idx = min((rmp1 - (uint32_t)h16) & 0xffffu, (uint32_t)(IW_SEXP_LUT - 1));
           }
-          uint32_t pw[4];
+          pb[r] = (uint32_t)sLut[idx];
+          if constexpr (!FULL) {
+            const int key = kbase0 + r;
+            bool ok = key < a.Tk;
+            if (HAS_MASK) ok = ok && q < a.Tq && !a.mask[(int64_t)q * a.Tk + key];
+            pb[r] &= ok ? 0xffu : 0u;
+          }
+        }
+        uint32_t pw[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            pw[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pb[4 * j + 3], pb[4 * j + 2], 0x0c0c0400u),
-                                          __builtin_amdgcn_perm(pb[4 * j + 1], pb[4 * j], 0x0c0c0400u),
-                                          0x05040100u);
-          const uint32_t ones = 0x01010101u;
-          psum = __builtin_amdgcn_udot4(pw[0], ones, psum, false);
-          psum = __builtin_amdgcn_udot4(pw[1], ones, psum, false);
-          psum = __builtin_amdgcn_udot4(pw[2], ones, psum, false);
-          psum = __builtin_amdgcn_udot4(pw[3], ones, psum, false);
-          // P <= 127 except at x_sub == 0 after an int16 row-max wrap (P = 128).
-          // int8 MFMA is signed, so such tiles split P = lo + 64 * hi2.
+        for (int j = 0; j < 4; ++j)
+          pw[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(pb[4 * j + 3], pb[4 * j + 2], 0x0c0c0400u),
+                                        __builtin_amdgcn_perm(pb[4 * j + 1], pb[4 * j], 0x0c0c0400u),
+                                        0x05040100u);
+        const uint32_t ones = 0x01010101u;
+        psum = __builtin_amdgcn_udot4(pw[0], ones, psum, false);
+        psum = __builtin_amdgcn_udot4(pw[1], ones, psum, false);
+        psum = __builtin_amdgcn_udot4(pw[2], ones, psum, false);
+        psum = __builtin_amdgcn_udot4(pw[3], ones, psum, false);
+        const v4i pa0 = v4i{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
+        if constexpr (FULL) {
+#pragma unroll
+          for (int t = 0; t < KS; ++t) {
+            const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + sub * 32 + g * 16]);
+            o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa0, vb, o[t], 0, 0, 0);
+          }
+        } else {
+          // int8 MFMA is signed: tiles with P = 128 split P = lo + 64 * hi2
           const uint32_t hib = (pw[0] | pw[1] | pw[2] | pw[3]) & 0x80808080u;
           const bool any_hi = __any(hib != 0u);
-          v4i pa, ph;
-          if (!any_hi) {
-            pa = v4i{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
-          } else {
+          v4i pa = pa0, ph;
+          if (any_hi) {
             pa = v4i{(int)(pw[0] & 0x7f7f7f7fu), (int)(pw[1] & 0x7f7f7f7fu),
                      (int)(pw[2] & 0x7f7f7f7fu), (int)(pw[3] & 0x7f7f7f7fu)};
             ph = v4i{(int)((pw[0] >> 1) & 0x40404040u), (int)((pw[1] >> 1) & 0x40404040u),
@@ -377,13 +444,15 @@ void attn_prefill_kernel(AttnArgs a) {
             }
           }
         }
-      };
-      if (!HAS_MASK && (kc + 1) * PF_KC <= a.Tk)
-        chunk(std::true_type{});
-      else
-        chunk(std::false_type{});
+      }
       __syncthreads();
-    }
+    };
+    // the split point is uniform over the wave; every wave of the block runs
+    // nkc iterations, so the barriers pair up
+    const int nfull2 = (!HAS_MASK && no_sat) ? a.Tk / PF_KC : 0;
+    int kc2 = 0;
+    for (; kc2 < nfull2; ++kc2) pass2(kc2, std::true_type{});
+    for (; kc2 < nkc; ++kc2) pass2(kc2, std::false_type{});
     psum += (uint32_t)__shfl_xor((int)psum, 32);
     if (g == 0) sInv[wave][ql] = fisr((int32_t)psum, a.rsqrt_off);
     __syncthreads();

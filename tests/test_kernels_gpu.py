@@ -401,6 +401,46 @@ def test_attention_fused_wrap_corner(iw, oracle, gpu, decode):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("qs", [0, 1, 9, 13, 14, 20, 27, 28, 29, 30, 31])
+def test_attention_prefill_requant_extremes(iw, oracle, gpu, D, qs):
+    """Scores at the int8 extremes (|QK^T| up to 128 * 128 * D) against every
+    requant shift and the multipliers 0, 1 and 255, over key chunks that are
+    full (64 keys) and a ragged last one: keys aligned with the query (largest
+    scores, saturating the int16 row maximum for small shifts), anti-aligned
+    (most negative) and random signs."""
+    B, H, Tq, Tk = 1, 2, 70, 150
+    r = gen.rng(1000 + 31 * D + qs)
+    q = np.where(r.random((B, H, Tq, D)) < 0.5, -128, 127).astype(np.int8)
+    k = np.where(r.random((B, H, Tk, D)) < 0.5, -128, 127).astype(np.int8)
+    for t in range(0, Tk, 5):
+        k[:, :, t] = q[:, :, t % Tq]           # aligned with query t % Tq
+    for t in range(2, Tk, 7):
+        k[:, :, t] = np.where(q[:, :, (t + 3) % Tq] < 0, 127, -128)  # anti-aligned
+    v = gen.i8(r, (B, H, D, Tk))
+    for qm in (0, 1, 255):
+        _print_case("attention prefill extremes", B, H, Tq, Tk, D, f"qs={qs} qm={qm}")
+        exp = oracle.attention(q, k, v, None, qm, qs, 8, 200, 6)
+        got = _fused(iw, q, k, v, None, qm, qs, 8, 200, 6, decode=False)
+        assert np.array_equal(got, exp), (qs, qm)
+
+
+def test_attention_prefill_wrap_in_full_chunks(iw, oracle, gpu):
+    """The row-maximum wrap (P = 128 at x_sub = 0) inside full 64-key chunks:
+    every query row saturates at +32767 while a third of the keys sit at
+    -32768."""
+    B, H, Tq, Tk, D = 1, 2, 33, 200, 64
+    q = np.full((B, H, Tq, D), 127, np.int8)
+    k = np.full((B, H, Tk, D), 127, np.int8)
+    k[..., 1::3, :] = -128
+    q[:, 1, 5:] = gen.i8(gen.rng(3), (B, Tq - 5, D))  # rows of head 1 past 5: no saturation
+    v = gen.i8(gen.rng(2), (B, H, D, Tk))
+    for qs in (0, 4):
+        exp = oracle.attention(q, k, v, None, 255, qs, 8, 200, 6)
+        got = _fused(iw, q, k, v, None, 255, qs, 8, 200, 6, decode=False)
+        assert np.array_equal(got, exp), qs
+
+
 def test_argmax_rows(iw, gpu):
     r = gen.rng(9)
     x = gen.i8(r, (7, 51865))
