@@ -3,9 +3,9 @@
 // and FC2 (+residual15), and any dense Linear with K % 64 == 0.
 //
 // C[m][n] = sum_k A[m][k] * B[n][k], both operands K-contiguous int8.
-// Block tile 256 (M) x 128 (N) x 64 (K); 4 waves in a 2 x 2 grid, each a
-// 128 x 64 tile of 4 x 2 v_mfma_i32_32x32x32_i8 blocks. Two blocks share a
-// CU so that one block's epilogue (VALU) overlaps the other's MFMAs.
+// Block tile 256 (M) x 256 (N) x 64 (K); 8 waves in a 2 x 4 grid, each a
+// 128 x 64 tile of 4 x 2 v_mfma_i32_32x32x32_i8 blocks; one block per CU
+// (two waves per SIMD).
 //
 // Operands stream global -> LDS without passing through registers, into a
 // 3-stage ring: while the MFMAs consume stage k, stages k+1 and k+2 are in
@@ -123,9 +123,13 @@ struct EpiCol {
 // BK: K bytes per stage (64: 3 x 72 KB rings, two blocks per CU; 128: every
 // wave-wide copy reads 8 whole 128-byte lines instead of 16 half lines,
 // 3 x 144 KB, one block per CU)
-template <int EPI, bool GELU, bool ZP, int BK>
+// GT: the GeLU parameters are one value for all columns, so GeLU is a
+// function of the int8 requantized value alone, applied as a 255-entry table
+// built in LDS once per block.
+template <int EPI, bool GELU, bool ZP, int BK, bool GT>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(BK == 64 ? 2 : 1, BK == 64 ? 2 : 1)))
 void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
+  static_assert(!GT || GELU, "the GeLU table needs the GeLU epilogue");
   constexpr int A_STAGE = BM * BK, B_STAGE = BN * BK;
   constexpr int CPR = BK / 16;              // 16-byte chunks per LDS row
   constexpr int RPI = 64 / CPR;             // rows per wave-wide copy
@@ -148,6 +152,7 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   __shared__ __attribute__((aligned(16))) uint32_t sPgim[BN], sPgih[BN], sPgom[BN], sPgoh[BN];
   __shared__ __attribute__((aligned(16))) int32_t sPgis[BN], sPgos[BN];
   __shared__ uint8_t sLut[16];
+  __shared__ uint8_t sGelu[GT ? 256 : 1];  // GeLU(y) at y + 127, y in [-127, 127]
 
   const int bid = blockIdx.x;
   const int tile = (bid % XCDS) * per_xcd + bid / XCDS;
@@ -331,14 +336,15 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
     const int32_t s = xs + __shfl_xor(xs, 32);
     if (lane < 32) sXsum[wm * 128 + wn * 32 + lane] = s;
   }
+  ColParams c;
   if (tid < BN) {
-    const ColParams c = decode_col<EPI>(g, craw);
+    c = decode_col<EPI>(g, craw);
     sPm[tid] = c.mult;
     sPh[tid] = c.shift.half;
     sPsh[tid] = (int32_t)c.shift.sh;
     sPnz[tid] = 0u - c.wz;
     sPb[tid] = c.bias;
-    if (GELU) {
+    if (GELU && !GT) {
       sPgim[tid] = c.gi_m;
       sPgih[tid] = c.gi_s.half;
       sPgis[tid] = (int32_t)c.gi_s.sh;
@@ -349,6 +355,11 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   }
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
   __syncthreads();
+  if (GT) {
+    // every column decodes the same GeLU parameters
+    if (tid < 255) sGelu[tid] = (uint8_t)gelu_dec(tid - 127, sLut, c);
+    __syncthreads();
+  }
 
   // Epilogue. The MFMAs take the B fragment as their first operand, so
   // acc[i][j] is the transposed 32x32 block: lane l holds row
@@ -422,7 +433,7 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
         }
         EpiShift gi[4], go[4];
         uint32_t gim[4], gom[4];
-        if (GELU) {
+        if (GELU && !GT) {
           const uint4 a = *reinterpret_cast<const uint4 *>(&sPgim[cw]);
           const uint4 b = *reinterpret_cast<const uint4 *>(&sPgih[cw]);
           const uint4 c = *reinterpret_cast<const uint4 *>(&sPgis[cw]);
@@ -442,7 +453,10 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
             int32_t y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = ec[e].requant8(acc[i][j][q * 4 + e], xsm[i]);
-            if (GELU) {
+            if (GT) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) y[e] = sGelu[y[e] + 127];
+            } else if (GELU) {
               int32_t t[4];
               uint8_t lv[4];
 #pragma unroll
@@ -504,7 +518,7 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
   }
 }
 
-template <int EPI, bool GELU>
+template <int EPI, bool GELU, bool GT = false>
 int launch_dtl(const GemmArgs &g, hipStream_t s) {
   const int64_t tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
   const int64_t tiles = tm * tn;
@@ -514,9 +528,11 @@ int launch_dtl(const GemmArgs &g, hipStream_t s) {
   // BK = 128 (whole 128-byte lines per copy, one block per CU) measured
   // slower than two blocks per CU with BK = 64
   if (g.wz)
-    hipLaunchKernelGGL((gemm_dtl_kernel<EPI, GELU, true, 64>), grid, block, 0, s, g, (int)tn, (int)tiles, per_xcd);
+    hipLaunchKernelGGL((gemm_dtl_kernel<EPI, GELU, true, 64, GT>), grid, block, 0, s, g, (int)tn, (int)tiles,
+                       per_xcd);
   else
-    hipLaunchKernelGGL((gemm_dtl_kernel<EPI, GELU, false, 64>), grid, block, 0, s, g, (int)tn, (int)tiles, per_xcd);
+    hipLaunchKernelGGL((gemm_dtl_kernel<EPI, GELU, false, 64, GT>), grid, block, 0, s, g, (int)tn, (int)tiles,
+                       per_xcd);
   return check_launch("gemm_dtl_kernel");
 }
 
@@ -539,8 +555,11 @@ bool gemm_dtl_eligible(const GemmArgs &g) {
 
 int gemm_dtl(const GemmArgs &g, hipStream_t s) {
   const bool gelu = g.lut != nullptr;
+  // one GeLU parameter set for all columns: the table form
+  const bool gtab = gelu && !g.luti_pc && !g.luto_pc;
   switch (g.epi) {
     case EPI_L8:
+      if (gtab) return launch_dtl<EPI_L8, true, true>(g, s);
       if (gelu) return launch_dtl<EPI_L8, true>(g, s);
       return launch_dtl<EPI_L8, false>(g, s);
     case EPI_L32: return launch_dtl<EPI_L32, false>(g, s);

@@ -90,9 +90,28 @@ def _ln(ln, x: torch.Tensor, rows: int, out: torch.Tensor):
     return out
 
 
-def _mlp_gelu(block: ResidualAttentionBlock_int, x_ptr: int, M: int, out: torch.Tensor):
-    fc1, gelu = block.mlp[0], block.mlp[1]
+def _gelu_args(gelu) -> tuple:
+    """GeLU parameter pointers and counts for the fused FC1 + GeLU GEMM. A
+    per-channel parameter whose values are all equal is passed as a single
+    value (count 1): the same results, and the large-M GEMM then applies GeLU
+    as a table of the int8 value. Reads the parameters once (a device sync),
+    so runners call it when they are built."""
     lut, im, is_, om, os_, ci, co = gelu.gelu_ptrs()
+
+    def uniform(t: torch.Tensor) -> bool:
+        return t.numel() > 1 and bool((t == t.reshape(-1)[0]).all())
+
+    if uniform(gelu.luti_req_multiplier) and uniform(gelu.luti_req_shiftmount):
+        ci = 1
+    if uniform(gelu.luto_req_multiplier) and uniform(gelu.luto_req_shiftmount):
+        co = 1
+    return lut, im, is_, om, os_, ci, co
+
+
+def _mlp_gelu(block: ResidualAttentionBlock_int, x_ptr: int, M: int, out: torch.Tensor,
+              gelu_args: Optional[tuple] = None):
+    fc1, gelu = block.mlp[0], block.mlp[1]
+    lut, im, is_, om, os_, ci, co = gelu_args if gelu_args is not None else gelu.gelu_ptrs()
     _lib.call("iw_linear8_gelu", x_ptr, fc1.weight.data_ptr(), _ptr(fc1.bias),
               _ptr(fc1.wgt_zeros), fc1.req_multiplier.data_ptr(), fc1.req_shiftmount.data_ptr(),
               lut, im, is_, om, os_, ci, co, out.data_ptr(), M, fc1.in_features, fc1.out_features,
@@ -183,6 +202,7 @@ class EncoderRunner:
         self.f8 = torch.empty((self.M, 4 * C), dtype=torch.int8, device=dev)
         self.out = torch.empty((batch, T, C), dtype=torch.int8, device=dev)
         self.tables = [b.attn.shift_exp_table() for b in encoder.blocks]
+        self.gelu_args = [_gelu_args(b.mlp[1]) for b in encoder.blocks]
         # Optional per-launch timing: a list receiving (kind, ops, start, end)
         # HIP events recorded on the launch stream around GEMM / attention calls.
         self.timer: Optional[list] = None
@@ -224,7 +244,7 @@ class EncoderRunner:
         self._tock(t)
         _ln(blk.mlp_ln, x16, M, self.h8)
         t = self._tick("gemm", 2.0 * M * 4 * C * C)
-        _mlp_gelu(blk, self.h8.data_ptr(), M, self.f8)
+        _mlp_gelu(blk, self.h8.data_ptr(), M, self.f8, self.gelu_args[i])
         self._tock(t)
         t = self._tick("gemm", 2.0 * M * 4 * C * C)
         _lin32_res(blk.mlp[2], self.f8.data_ptr(), M, x16, sc["m"])

@@ -51,13 +51,16 @@ def test_linear32_big(iw, oracle, gpu, M, K, N):
     assert np.array_equal(host(got), oracle.linear32(x, w, b, z, m, s))
 
 
-@pytest.mark.parametrize("M,K,N", [(8300, 1280, 300), (BIG_ROWS, 384, 1536)])
-@pytest.mark.parametrize("pc", [True, False])
-def test_linear8_gelu_big(iw, oracle, gpu, M, K, N, pc):
-    print("case: linear8_gelu_big", M, K, N, pc, flush=True)
+@pytest.mark.parametrize("M,K,N,pci,pco", [(8300, 1280, 300, True, True), (8300, 1280, 300, False, False),
+                                           (8300, 1280, 300, False, True), (8300, 1280, 300, True, False),
+                                           (BIG_ROWS, 384, 1536, True, True), (BIG_ROWS, 384, 1536, False, False)])
+def test_linear8_gelu_big(iw, oracle, gpu, M, K, N, pci, pco):
+    """Per-channel and per-tensor GeLU parameters (both per-tensor: the GEMM
+    applies GeLU as a table of the int8 value)."""
+    print("case: linear8_gelu_big", M, K, N, pci, pco, flush=True)
     x, w, b, z, m, s = gen.realistic_linear_case(M + K + 3 * N, M, K, N)
-    r = gen.rng(M * N + pc)
-    lut, im, is_, om, os_ = gen.gelu_params(r, N, pc, pc)
+    r = gen.rng(M * N + pci + 2 * pco)
+    lut, im, is_, om, os_ = gen.gelu_params(r, N, pci, pco)
     got = iw.kernels.linear8_gelu_hip(T(x), T(w), T(b), T(z), T(m), T(s), T(lut), T(im), T(is_),
                                       T(om), T(os_))
     exp = oracle.gelu(oracle.linear8(x, w, b, z, m, s), lut, im, is_, om, os_)
