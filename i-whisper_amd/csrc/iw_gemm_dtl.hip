@@ -22,6 +22,8 @@
 // fragments already in registers (the two waves sharing rows split the
 // subtiles). Epilogues are those of iw_gemm_dev.hpp, bit-identical to the
 // reference kernels.
+#include <type_traits>
+
 #include "iw_gemm_dev.hpp"
 
 namespace iw {
@@ -354,168 +356,180 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
     }
   }
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
-  __syncthreads();
+  // any multiplier of the tile's columns at or above 2^31 (the signed x
+  // unsigned high product then needs its correction term)
+  const bool big_m = __syncthreads_or(tid < BN && (c.mult >> 31) != 0u);
   if (GT) {
     // every column decodes the same GeLU parameters
     if (tid < 255) sGelu[tid] = (uint8_t)gelu_dec(tid - 127, sLut, c);
     __syncthreads();
   }
 
-  // Epilogue. The MFMAs take the B fragment as their first operand, so
-  // acc[i][j] is the transposed 32x32 block: lane l holds row
-  // m = i*32 + l%32 of the wave tile and, for register r, column
-  // n = j*32 + (r/4)*8 + (l/32)*4 + r%4, i.e. four consecutive columns per
-  // register group. Phase A applies the integer epilogue to four columns at a
-  // time and writes the results into the wave's region of the (now idle)
-  // ring; phase B reads that region back row-contiguously and stores whole
-  // 16-byte pieces (rows past M fall outside the buffer range and are
-  // dropped by the hardware; N % 16 == 0 keeps every piece inside or outside
-  // the matrix as a whole).
-  constexpr int OB = (EPI == EPI_L8 || EPI == EPI_S8) ? 1 : (EPI == EPI_L32 ? 4 : 2);
-  constexpr bool BYTES = OB == 1;  // staged values: int8 results, else int32 pre-residual
-  constexpr int SROW = BYTES ? 64 + 16 : 256 + 16;  // staging row bytes (padded)
-  constexpr int HALVES = BYTES ? 1 : WN;            // int32 staging: 128 / WN rows at a time
-  constexpr int SROWS = 128 / HALVES;
-  static_assert(NWAVES * SROWS * SROW <= STAGES * (A_STAGE + B_STAGE), "staging fits in the ring");
-  int8_t *const stage = sMem + wave * SROWS * SROW;
-  const int ldo = (int)g.ldc * OB;
-  const __amdgpu_buffer_rsrc_t out_rs = __builtin_amdgcn_make_buffer_rsrc(
-      reinterpret_cast<char *>(g.out) + ((int64_t)m0 * g.ldc + n0) * OB, (short)0,
-      (int)min((int64_t)(M - m0) * ldo, (int64_t)0x7fffffff), kBufferFlags);
-  const int ldr = (int)g.ldres * 2;
-  __amdgpu_buffer_rsrc_t res_rs = out_rs;
-  if (EPI == EPI_L32RES)
-    res_rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int16_t *>(g.res) + (int64_t)m0 * g.ldres + n0, (short)0,
-        (int)min((int64_t)(M - m0) * ldr, (int64_t)0x7fffffff), kBufferFlags);
-  int32_t xsm[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) xsm[i] = zp ? sXsum[wm * 128 + i * 32 + (lane & 31)] : 0;
+  // The epilogue is instantiated twice: without the high-product correction
+  // (every multiplier below 2^31, the usual case) and with it.
+  auto epilogue = [&](auto big_tag) {
+    constexpr bool BIG = decltype(big_tag)::value;
+    // Epilogue. The MFMAs take the B fragment as their first operand, so
+    // acc[i][j] is the transposed 32x32 block: lane l holds row
+    // m = i*32 + l%32 of the wave tile and, for register r, column
+    // n = j*32 + (r/4)*8 + (l/32)*4 + r%4, i.e. four consecutive columns per
+    // register group. Phase A applies the integer epilogue to four columns at a
+    // time and writes the results into the wave's region of the (now idle)
+    // ring; phase B reads that region back row-contiguously and stores whole
+    // 16-byte pieces (rows past M fall outside the buffer range and are
+    // dropped by the hardware; N % 16 == 0 keeps every piece inside or outside
+    // the matrix as a whole).
+    constexpr int OB = (EPI == EPI_L8 || EPI == EPI_S8) ? 1 : (EPI == EPI_L32 ? 4 : 2);
+    constexpr bool BYTES = OB == 1;  // staged values: int8 results, else int32 pre-residual
+    constexpr int SROW = BYTES ? 64 + 16 : 256 + 16;  // staging row bytes (padded)
+    constexpr int HALVES = BYTES ? 1 : WN;            // int32 staging: 128 / WN rows at a time
+    constexpr int SROWS = 128 / HALVES;
+    static_assert(NWAVES * SROWS * SROW <= STAGES * (A_STAGE + B_STAGE), "staging fits in the ring");
+    int8_t *const stage = sMem + wave * SROWS * SROW;
+    const int ldo = (int)g.ldc * OB;
+    const __amdgpu_buffer_rsrc_t out_rs = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<char *>(g.out) + ((int64_t)m0 * g.ldc + n0) * OB, (short)0,
+        (int)min((int64_t)(M - m0) * ldo, (int64_t)0x7fffffff), kBufferFlags);
+    const int ldr = (int)g.ldres * 2;
+    __amdgpu_buffer_rsrc_t res_rs = out_rs;
+    if (EPI == EPI_L32RES)
+      res_rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int16_t *>(g.res) + (int64_t)m0 * g.ldres + n0, (short)0,
+          (int)min((int64_t)(M - m0) * ldr, (int64_t)0x7fffffff), kBufferFlags);
+    int32_t xsm[4];
+  #pragma unroll
+    for (int i = 0; i < 4; ++i) xsm[i] = zp ? sXsum[wm * 128 + i * 32 + (lane & 31)] : 0;
 
-  constexpr int PPR = BYTES ? 4 : 16;  // 16-byte staged pieces per row
-  constexpr int PIECES = SROWS * PPR / 64;  // pieces per lane per half
-#pragma unroll
-  for (int hf = 0; hf < HALVES; ++hf) {
-    const int row0 = wm * 128 + hf * SROWS;  // tile-local first row of this half
-    // The residual rows of this half are requested before phase A so their
-    // latency hides behind the requantization (in-place calls: these rows
-    // are stored only after they are read, and the other half's rows are
-    // disjoint).
-    u32x2 rpre[EPI == EPI_L32RES ? PIECES : 1];
-    if (EPI == EPI_L32RES) {
-#pragma unroll
-      for (int t = 0; t < PIECES; ++t) {
-        const int pc = lane + 64 * t;
-        const int col = wn * 64 + (pc % PPR) * 4;
-        const int roff = n0 + col < N ? (row0 + pc / PPR) * ldr + col * 2 : (int)0x80000000;
-        rpre[t] = __builtin_amdgcn_raw_buffer_load_b64(res_rs, roff, 0, 0);
+    constexpr int PPR = BYTES ? 4 : 16;  // 16-byte staged pieces per row
+    constexpr int PIECES = SROWS * PPR / 64;  // pieces per lane per half
+  #pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+      const int row0 = wm * 128 + hf * SROWS;  // tile-local first row of this half
+      // The residual rows of this half are requested before phase A so their
+      // latency hides behind the requantization (in-place calls: these rows
+      // are stored only after they are read, and the other half's rows are
+      // disjoint).
+      u32x2 rpre[EPI == EPI_L32RES ? PIECES : 1];
+      if (EPI == EPI_L32RES) {
+  #pragma unroll
+        for (int t = 0; t < PIECES; ++t) {
+          const int pc = lane + 64 * t;
+          const int col = wn * 64 + (pc % PPR) * 4;
+          const int roff = n0 + col < N ? (row0 + pc / PPR) * ldr + col * 2 : (int)0x80000000;
+          rpre[t] = __builtin_amdgcn_raw_buffer_load_b64(res_rs, roff, 0, 0);
+        }
       }
-    }
-    // ---- phase A: results of rows [hf*SROWS, +SROWS) of the wave tile ----
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int cl = j * 32 + q * 8 + (lane >> 5) * 4;  // first of 4 columns, wave-local
-        const int cw = wn * 64 + cl;                     // tile-local
-        const uint4 pm = *reinterpret_cast<const uint4 *>(&sPm[cw]);
-        const uint4 psh = *reinterpret_cast<const uint4 *>(&sPsh[cw]);
-        const uint4 pnz = *reinterpret_cast<const uint4 *>(&sPnz[cw]);
-        const uint4 pb = *reinterpret_cast<const uint4 *>(&sPb[cw]);
-        EpiCol ec[4];
-        ec[0].set(pm.x, psh.x, pnz.x, pb.x);
-        ec[1].set(pm.y, psh.y, pnz.y, pb.y);
-        ec[2].set(pm.z, psh.z, pnz.z, pb.z);
-        ec[3].set(pm.w, psh.w, pnz.w, pb.w);
-        if (BYTES) {
-          const uint4 ph = *reinterpret_cast<const uint4 *>(&sPh[cw]);
-          ec[0].half = ph.x, ec[1].half = ph.y, ec[2].half = ph.z, ec[3].half = ph.w;
-        }
-        EpiShift gi[4], go[4];
-        uint32_t gim[4], gom[4];
-        if (GELU && !GT) {
-          const uint4 a = *reinterpret_cast<const uint4 *>(&sPgim[cw]);
-          const uint4 b = *reinterpret_cast<const uint4 *>(&sPgih[cw]);
-          const uint4 c = *reinterpret_cast<const uint4 *>(&sPgis[cw]);
-          const uint4 d = *reinterpret_cast<const uint4 *>(&sPgom[cw]);
-          const uint4 e = *reinterpret_cast<const uint4 *>(&sPgoh[cw]);
-          const uint4 f = *reinterpret_cast<const uint4 *>(&sPgos[cw]);
-          gim[0] = a.x, gim[1] = a.y, gim[2] = a.z, gim[3] = a.w;
-          gom[0] = d.x, gom[1] = d.y, gom[2] = d.z, gom[3] = d.w;
-          gi[0].set(b.x, c.x), gi[1].set(b.y, c.y), gi[2].set(b.z, c.z), gi[3].set(b.w, c.w);
-          go[0].set(e.x, f.x), go[1].set(e.y, f.y), go[2].set(e.z, f.z), go[3].set(e.w, f.w);
-        }
-#pragma unroll
-        for (int ii = 0; ii < 4 / HALVES; ++ii) {
-          const int i = hf * (4 / HALVES) + ii;
-          const int srow = ii * 32 + (lane & 31);  // staging row
+      // ---- phase A: results of rows [hf*SROWS, +SROWS) of the wave tile ----
+  #pragma unroll
+      for (int j = 0; j < 2; ++j) {
+  #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cl = j * 32 + q * 8 + (lane >> 5) * 4;  // first of 4 columns, wave-local
+          const int cw = wn * 64 + cl;                     // tile-local
+          const uint4 pm = *reinterpret_cast<const uint4 *>(&sPm[cw]);
+          const uint4 psh = *reinterpret_cast<const uint4 *>(&sPsh[cw]);
+          const uint4 pnz = *reinterpret_cast<const uint4 *>(&sPnz[cw]);
+          const uint4 pb = *reinterpret_cast<const uint4 *>(&sPb[cw]);
+          EpiCol ec[4];
+          ec[0].set(pm.x, psh.x, pnz.x, pb.x);
+          ec[1].set(pm.y, psh.y, pnz.y, pb.y);
+          ec[2].set(pm.z, psh.z, pnz.z, pb.z);
+          ec[3].set(pm.w, psh.w, pnz.w, pb.w);
+          if (!BIG) ec[0].mneg = ec[1].mneg = ec[2].mneg = ec[3].mneg = 0u;
           if (BYTES) {
-            int32_t y[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = ec[e].requant8(acc[i][j][q * 4 + e], xsm[i]);
-            if (GT) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) y[e] = sGelu[y[e] + 127];
-            } else if (GELU) {
-              int32_t t[4];
-              uint8_t lv[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                t[e] = min(max(gi[e].apply((uint32_t)__mul24(y[e], (int32_t)gim[e])), -8), 7);
-                lv[e] = sLut[t[e] + 8];
+            const uint4 ph = *reinterpret_cast<const uint4 *>(&sPh[cw]);
+            ec[0].half = ph.x, ec[1].half = ph.y, ec[2].half = ph.z, ec[3].half = ph.w;
+          }
+          EpiShift gi[4], go[4];
+          uint32_t gim[4], gom[4];
+          if (GELU && !GT) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(&sPgim[cw]);
+            const uint4 b = *reinterpret_cast<const uint4 *>(&sPgih[cw]);
+            const uint4 c = *reinterpret_cast<const uint4 *>(&sPgis[cw]);
+            const uint4 d = *reinterpret_cast<const uint4 *>(&sPgom[cw]);
+            const uint4 e = *reinterpret_cast<const uint4 *>(&sPgoh[cw]);
+            const uint4 f = *reinterpret_cast<const uint4 *>(&sPgos[cw]);
+            gim[0] = a.x, gim[1] = a.y, gim[2] = a.z, gim[3] = a.w;
+            gom[0] = d.x, gom[1] = d.y, gom[2] = d.z, gom[3] = d.w;
+            gi[0].set(b.x, c.x), gi[1].set(b.y, c.y), gi[2].set(b.z, c.z), gi[3].set(b.w, c.w);
+            go[0].set(e.x, f.x), go[1].set(e.y, f.y), go[2].set(e.z, f.z), go[3].set(e.w, f.w);
+          }
+  #pragma unroll
+          for (int ii = 0; ii < 4 / HALVES; ++ii) {
+            const int i = hf * (4 / HALVES) + ii;
+            const int srow = ii * 32 + (lane & 31);  // staging row
+            if (BYTES) {
+              int32_t y[4];
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) y[e] = ec[e].requant8(acc[i][j][q * 4 + e], xsm[i]);
+              if (GT) {
+  #pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = sGelu[y[e] + 127];
+              } else if (GELU) {
+                int32_t t[4];
+                uint8_t lv[4];
+  #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  t[e] = min(max(gi[e].apply((uint32_t)__mul24(y[e], (int32_t)gim[e])), -8), 7);
+                  lv[e] = sLut[t[e] + 8];
+                }
+  #pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  y[e] = clampi(go[e].apply((uint32_t)__mul24(__mul24(y[e], (int32_t)lv[e]), (int32_t)gom[e])), -127, 127);
               }
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                y[e] = clampi(go[e].apply((uint32_t)__mul24(__mul24(y[e], (int32_t)lv[e]), (int32_t)gom[e])), -127, 127);
+              // bytes y0..y3 (selector 0x0c gives a zero byte)
+              const uint32_t lo = __builtin_amdgcn_perm((uint32_t)y[1], (uint32_t)y[0], 0x0c0c0400u);
+              const uint32_t hi = __builtin_amdgcn_perm((uint32_t)y[3], (uint32_t)y[2], 0x0c0c0400u);
+              const uint32_t packed = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+              *reinterpret_cast<uint32_t *>(stage + srow * SROW + cl) = packed;
+            } else {
+              uint32_t br[4];
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) br[e] = ec[e].pre_residual(acc[i][j][q * 4 + e], xsm[i]);
+              *reinterpret_cast<uint4 *>(stage + srow * SROW + cl * 4) = make_uint4(br[0], br[1], br[2], br[3]);
             }
-            // bytes y0..y3 (selector 0x0c gives a zero byte)
-            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)y[1], (uint32_t)y[0], 0x0c0c0400u);
-            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)y[3], (uint32_t)y[2], 0x0c0c0400u);
-            const uint32_t packed = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-            *reinterpret_cast<uint32_t *>(stage + srow * SROW + cl) = packed;
-          } else {
-            uint32_t br[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) br[e] = ec[e].pre_residual(acc[i][j][q * 4 + e], xsm[i]);
-            *reinterpret_cast<uint4 *>(stage + srow * SROW + cl * 4) = make_uint4(br[0], br[1], br[2], br[3]);
           }
         }
       }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back its own region
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back its own region
 
-    // ---- phase B: 16-byte pieces of the staged rows to global memory ----
-#pragma unroll
-    for (int t = 0; t < PIECES; ++t) {
-      const int pc = lane + 64 * t;
-      const int r = pc / PPR, c = pc % PPR;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * SROW + c * 16);
-      const int col = wn * 64 + c * (BYTES ? 16 : 4);  // tile-local first column
-      const bool ok = n0 + col < N;
-      const int rr = row0 + r;
-      if (BYTES) {
-        const int off = ok ? rr * ldo + col : (int)0x80000000;
-        __builtin_amdgcn_raw_buffer_store_b128(v, out_rs, off, 0, 0);
-      } else if (EPI == EPI_L32) {
-        const int off = ok ? rr * ldo + col * 4 : (int)0x80000000;
-        __builtin_amdgcn_raw_buffer_store_b128(v, out_rs, off, 0, 0);
-      } else {
-        const u32x2 rv = rpre[t];
-        const int32_t res[4] = {(int16_t)(rv[0] & 0xffff), (int16_t)(rv[0] >> 16), (int16_t)(rv[1] & 0xffff),
-                                (int16_t)(rv[1] >> 16)};
-        const uint32_t brv[4] = {v[0], v[1], v[2], v[3]};
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t s = brv[e] + (uint32_t)__mul24(res[e], (int32_t)g.res_mult);
-          o[e] = (uint32_t)(uint16_t)clampi(rshift_pos((int32_t)s, 15), -16383, 16383);
+      // ---- phase B: 16-byte pieces of the staged rows to global memory ----
+  #pragma unroll
+      for (int t = 0; t < PIECES; ++t) {
+        const int pc = lane + 64 * t;
+        const int r = pc / PPR, c = pc % PPR;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * SROW + c * 16);
+        const int col = wn * 64 + c * (BYTES ? 16 : 4);  // tile-local first column
+        const bool ok = n0 + col < N;
+        const int rr = row0 + r;
+        if (BYTES) {
+          const int off = ok ? rr * ldo + col : (int)0x80000000;
+          __builtin_amdgcn_raw_buffer_store_b128(v, out_rs, off, 0, 0);
+        } else if (EPI == EPI_L32) {
+          const int off = ok ? rr * ldo + col * 4 : (int)0x80000000;
+          __builtin_amdgcn_raw_buffer_store_b128(v, out_rs, off, 0, 0);
+        } else {
+          const u32x2 rv = rpre[t];
+          const int32_t res[4] = {(int16_t)(rv[0] & 0xffff), (int16_t)(rv[0] >> 16), (int16_t)(rv[1] & 0xffff),
+                                  (int16_t)(rv[1] >> 16)};
+          const uint32_t brv[4] = {v[0], v[1], v[2], v[3]};
+          uint32_t o[4];
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t s = brv[e] + (uint32_t)__mul24(res[e], (int32_t)g.res_mult);
+            o[e] = (uint32_t)(uint16_t)clampi(rshift_pos((int32_t)s, 15), -16383, 16383);
+          }
+          const int off = ok ? rr * ldo + col * 2 : (int)0x80000000;
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)}, out_rs, off, 0, 0);
         }
-        const int off = ok ? rr * ldo + col * 2 : (int)0x80000000;
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)}, out_rs, off, 0, 0);
       }
+      if (HALVES > 1) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next half
     }
-    if (HALVES > 1) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // region reused by the next half
-  }
+  };
+  if (big_m)
+    epilogue(std::true_type{});
+  else
+    epilogue(std::false_type{});
 }
 
 template <int EPI, bool GELU, bool GT = false>
