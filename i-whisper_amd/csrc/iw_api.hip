@@ -614,7 +614,7 @@ int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, i
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
       cus = v;
   }
-  return launch_attn_prefill(a, cus * 3, as_stream(stream));
+  return launch_attn_prefill(a, cus * (head_dim <= 64 ? 4 : 3), as_stream(stream));
 }
 
 int iw_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,

@@ -162,15 +162,25 @@ __device__ __forceinline__ int key_row(int kk) {
 }
 
 template <int KS, bool HAS_MASK>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 3 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 4 : 1)))
 void attn_prefill_kernel(AttnArgs a) {
   constexpr int DP = KS * 32;           // padded head dim
-  constexpr int KLD = DP + 16;          // sK row stride
-  constexpr int VLD = PF_KC + 16;       // sVt row stride
+  // K and V^T rows of 4 chunks of 16 bytes (head_dim 64) are unpadded, with
+  // chunk c of row r stored at position c ^ ((r >> 2) & 3): the 16 rows one
+  // 16-lane pass of a fragment read touches then cover the 64 banks once.
+  // That keeps a block at 40 KB of LDS (the table, one K and one V^T stage),
+  // four blocks per CU. Other head sizes pad each row by 16 bytes instead.
+  constexpr bool SWZ = KS == 2;
+  constexpr int KLD = SWZ ? DP : DP + 16;           // sK row stride
+  constexpr int VLD = SWZ ? PF_KC : PF_KC + 16;     // sVt row stride
+  auto kpos = [](int row, int chunk) { return SWZ ? (chunk ^ ((row >> 2) & 3)) : chunk; };
   __shared__ __attribute__((aligned(16))) uint8_t sLut[IW_SEXP_LUT];
   __shared__ __attribute__((aligned(16))) int8_t sK[PF_KC * KLD];
   __shared__ __attribute__((aligned(16))) int8_t sVt[DP * VLD];
-  __shared__ int32_t sInv[4][32];
+  // the per-row reciprocal square roots of a tile go to sK once its last
+  // chunk is consumed
+  int32_t(*const sInv)[32] = reinterpret_cast<int32_t(*)[32]>(sK);
+  static_assert(PF_KC * KLD >= 4 * 32 * 4, "sK holds the tile's 128 row factors");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, ql = lane & 31;
@@ -237,7 +247,7 @@ void attn_prefill_kernel(AttnArgs a) {
         if (c < PF_KC * CPK) {
           const int kk = c / CPK, part = c % CPK;
           const int row = (kk & 32) + key_row(kk & 31);
-          *reinterpret_cast<uint4 *>(&sK[row * KLD + part * 16]) = kv[j];
+          *reinterpret_cast<uint4 *>(&sK[row * KLD + kpos(row, part) * 16]) = kv[j];
         }
       }
     };
@@ -257,7 +267,7 @@ void attn_prefill_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
         const int c = tid + 256 * j;
-        if (c < DP * 4) *reinterpret_cast<uint4 *>(&sVt[(c >> 2) * VLD + (c & 3) * 16]) = vv[j];
+        if (c < DP * 4) *reinterpret_cast<uint4 *>(&sVt[(c >> 2) * VLD + kpos(c >> 2, c & 3) * 16]) = vv[j];
       }
     };
     auto scores = [&](int sub) {
@@ -266,7 +276,7 @@ void attn_prefill_kernel(AttnArgs a) {
       for (int r = 0; r < 16; ++r) s[r] = 0;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const v4i ka = *reinterpret_cast<const v4i *>(&sK[(sub * 32 + ql) * KLD + ks * 32 + g * 16]);
+        const v4i ka = *reinterpret_cast<const v4i *>(&sK[(sub * 32 + ql) * KLD + kpos(sub * 32 + ql, ks * 2 + g) * 16]);
         s = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka, qf[ks], s, 0, 0, 0);
       }
       return s;
@@ -287,15 +297,9 @@ void attn_prefill_kernel(AttnArgs a) {
         load_k(0);
         load_v(0);
       }
-      // both sub-blocks' scores first: the second MFMA pair runs while the
-      // first sub-block's maximum is taken
-      v16i sc[2];
-      sc[0] = scores(0);
-      if constexpr (FULL) sc[1] = scores(1);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
-        if (!FULL && sub == 1) sc[1] = scores(1);
-        const v16i s = sc[sub];
+        const v16i s = scores(sub);
         if constexpr (FULL) {
 #pragma unroll
           for (int r = 0; r < 16; r += 2) mx = max(max(mx, s[r]), s[r + 1]);
@@ -367,15 +371,9 @@ void attn_prefill_kernel(AttnArgs a) {
         load_k(kc + 1);
         load_v(kc + 1);
       }
-      // full chunks issue the second sub-block's score MFMAs ahead of the
-      // first sub-block's softmax, so they run under its VALU work
-      v16i sc[2];
-      sc[0] = scores(0);
-      if constexpr (FULL) sc[1] = scores(1);
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
-        if (!FULL && sub == 1) sc[1] = scores(1);
-        const v16i s = sc[sub];
+        const v16i s = scores(sub);
         const int kbase0 = kc * PF_KC + sub * 32 + g * 16;
         // P of the 16 keys: requant (24-bit product: |score| < 2^21 and an
         // 8-bit multiplier), round-half-away shift, int16 saturation, then
@@ -419,7 +417,7 @@ void attn_prefill_kernel(AttnArgs a) {
         if constexpr (FULL) {
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + sub * 32 + g * 16]);
+            const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + kpos(t * 32 + ql, sub * 2 + g) * 16]);
             o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa0, vb, o[t], 0, 0, 0);
           }
         } else {
@@ -435,7 +433,7 @@ void attn_prefill_kernel(AttnArgs a) {
           }
 #pragma unroll
           for (int t = 0; t < KS; ++t) {
-            const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + sub * 32 + g * 16]);
+            const v4i vb = *reinterpret_cast<const v4i *>(&sVt[(t * 32 + ql) * VLD + kpos(t * 32 + ql, sub * 2 + g) * 16]);
             o[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pa, vb, o[t], 0, 0, 0);
             if (any_hi) {
               // 128 * hi = 64 * hi + 64 * hi
