@@ -67,6 +67,22 @@ def test_linear8_gelu_big(iw, oracle, gpu, M, K, N, pci, pco):
     assert np.array_equal(host(got), exp)
 
 
+@pytest.mark.parametrize("ishift,oshift,im,om", [(40, 7, 200, 255), (-3, 33, 1, 128), (0, 0, 255, 255), (13, -1, 0, 77)])
+def test_linear8_gelu_big_table_edge_params(iw, oracle, gpu, ishift, oshift, im, om):
+    """One GeLU parameter set for all columns (the table form) with shifts
+    outside [0, 31] and zero multipliers, which the decoding clamps."""
+    M, K, N = 8300, 640, 160
+    print("case: linear8_gelu_big table", ishift, oshift, im, om, flush=True)
+    x, w, b, z, m, s = gen.realistic_linear_case(M + ishift + 7 * oshift, M, K, N)
+    lut = np.sort(gen.rng(5).integers(0, 256, size=16)).astype(np.uint8)
+    pi = (np.array([im], np.uint8), np.array([ishift], np.int8))
+    po = (np.array([om], np.uint8), np.array([oshift], np.int8))
+    got = iw.kernels.linear8_gelu_hip(T(x), T(w), T(b), T(z), T(m), T(s), T(lut), T(pi[0]), T(pi[1]),
+                                      T(po[0]), T(po[1]))
+    exp = oracle.gelu(oracle.linear8(x, w, b, z, m, s), lut, pi[0], pi[1], po[0], po[1])
+    assert np.array_equal(host(got), exp)
+
+
 @pytest.mark.parametrize("M,K,N", [(8300, 2048, 200), (BIG_ROWS + 100, 5120, 128)])
 def test_linear32_residual15_big(iw, oracle, gpu, M, K, N):
     print("case: linear32_residual15_big", M, K, N, flush=True)
