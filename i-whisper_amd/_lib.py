@@ -46,12 +46,12 @@ SIGNATURES = {
     "iw_attention": [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
                      _p, _i64, _i64, _i64, _i64, _i64, _u8, _i8, _i32, _u8, _i8, _u32, _p, _b, _p],
     "iw_argmax_rows": [_p, _i64, _i64, _i64, _p, _p],
-    "iw_transpose_heads": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "iw_transpose_heads": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "iw_copy_rows": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "iw_gather_heads": [_p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "iw_linear8_qkv_cache": [_p, _p, _p, _p, _p, _p, _i64, _i64, _b, _b, _p, _i64, _p, _i64, _i64,
-                             _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
-    "iw_attention_decode_cache": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
+                             _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "iw_attention_decode_cache": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64,
                                   _i64, _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32,
                                   _p],
     "iw_embed_tokens": [_p, _p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _p],
@@ -72,11 +72,12 @@ SIGNATURES = {
                              _i64, _b, _b, _b, _p, _i64, _i64, _p],
     "iw_linear32_residual15_frag": [_p, _p, _p, _p, _p, _p, _p, _u16, _p, _i64, _i64, _i64, _b, _b, _p],
     "iw_linear8_qkv_cache_frag": [_p, _p, _p, _p, _p, _p, _i64, _i64, _b, _b, _p, _i64, _p, _i64, _i64,
-                                  _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+                                  _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "iw_layernorm32_frag": [_p, _p, _p, _u8, _i8, _u32, _i8, _u32, _p, _i64, _i64, _b, _p, _i64, _i64,
                             _p],
-    "iw_attention_decode_cache_frag": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64,
-                                       _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32, _p],
+    "iw_attention_decode_cache_frag": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p,
+                                       _i64, _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32,
+                                       _p],
     "iw_classifier_frag": [_p, _p, _u32, _i8, _p, _i64, _i64, _i64, _p],
 }
 

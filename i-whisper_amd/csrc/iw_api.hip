@@ -76,9 +76,9 @@ int check_gelu_counts(int64_t channels, int64_t luti_count, int64_t luto_count) 
 int qkv_cache_args(const int8_t *x, const int8_t *weight, const int32_t *bias, const int8_t *weight_zero,
                    const uint32_t *multiplier, const int8_t *shift, int64_t M, int64_t K, bool has_bias,
                    bool asymmetric, int8_t *q_out, int64_t q_ld, int8_t *k_cache, int64_t k_sb, int64_t k_sh,
-                   int64_t k_st, int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
-                   int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions, const int32_t *pos,
-                   GemmArgs *g, SkinnyScatter *sc) {
+                   int64_t k_st, int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t v_sq,
+                   int64_t channels, int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
+                   const int32_t *pos, GemmArgs *g, SkinnyScatter *sc) {
   const int64_t N = 3 * channels;
   int rc = check_linear(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N, has_bias,
                         asymmetric);
@@ -89,8 +89,12 @@ int qkv_cache_args(const int8_t *x, const int8_t *weight, const int32_t *bias, c
   IW_REQUIRE(channels <= 0x3fffffff && tokens_per_row_group > 0 && M % tokens_per_row_group == 0,
              "rows must be whole groups of tokens_per_row_group");
   IW_REQUIRE(k_cache && v_cache && pos, "null cache pointer");
-  IW_REQUIRE(cache_positions > 0 && cache_positions <= 0x7fffffff && cache_positions <= v_sd,
-             "cache_positions must be positive and fit the transposed V rows");
+  IW_REQUIRE(cache_positions > 0 && cache_positions <= 0x7fffffff, "cache_positions must be positive");
+  // V transposed per head (the rows hold every position) or in key quads
+  // (a quad holds every d of the head)
+  IW_REQUIRE((v_sq == 4 && cache_positions <= v_sd) || (v_sd == 4 && v_sq >= 4 * head_dim),
+             "V cache: v_sq == 4 with transposed rows of at least cache_positions bytes, "
+             "or v_sd == 4 with v_sq >= 4 * head_dim (key quads)");
   *g = linear_args(x, weight, bias, weight_zero, multiplier, shift, q_out, M, K, N, has_bias, asymmetric,
                    EPI_L8);
   sc->q = q_out;
@@ -103,6 +107,7 @@ int qkv_cache_args(const int8_t *x, const int8_t *weight, const int32_t *bias, c
   sc->v_sb = v_sb;
   sc->v_sh = v_sh;
   sc->v_sd = v_sd;
+  sc->v_sq = v_sq;
   sc->C = (int)channels;
   sc->D = (int)head_dim;
   sc->T = (int)tokens_per_row_group;
@@ -130,7 +135,8 @@ int layernorm32_entry(const int16_t *x, const int8_t *weight, const int32_t *bia
 
 int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb, int64_t k_sh,
                                  int64_t k_st, const int8_t *vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
-                                 int8_t *out, int64_t o_sb, int64_t batch, int64_t heads, int64_t head_dim,
+                                 int64_t v_sq, int8_t *out, int64_t o_sb, int64_t batch, int64_t heads,
+                                 int64_t head_dim,
                                  int64_t k_length, const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                                  int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
                                  uint32_t rsqrt_offset, bool out_frag, iw_stream_t stream) {
@@ -143,13 +149,19 @@ int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k,
   // the key count on the device is k_length + *pos <= max_keys
   IW_REQUIRE(max_keys >= k_length && max_keys <= kDecodeCacheMaxKeys && (pos || max_keys == k_length),
              "at most 4096 keys, and max_keys bounds k_length + *pos");
-  IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((max_keys + 15) / 16) * 16,
-             "transposed V rows must be 16-byte multiples covering max_keys");
+  const bool quads = v_sq != 4;
+  if (quads)
+    IW_REQUIRE(v_sd == 4 && v_sq % 16 == 0 && v_sq >= 4 * head_dim && head_dim == 64,
+               "V in key quads needs v_sd == 4, v_sq >= 4 * head_dim, v_sq % 16 == 0 and head_dim 64");
+  else
+    IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((max_keys + 15) / 16) * 16,
+               "transposed V rows must be 16-byte multiples covering max_keys");
   if (batch == 0) return IW_OK;
   IW_REQUIRE(q && k && vt && out, "null tensor pointer");
   const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                           reinterpret_cast<uintptr_t>(vt) | (uintptr_t)q_sb | (uintptr_t)k_sb |
-                          (uintptr_t)k_sh | (uintptr_t)k_st | (uintptr_t)v_sb | (uintptr_t)v_sh;
+                          (uintptr_t)k_sh | (uintptr_t)k_st | (uintptr_t)v_sb | (uintptr_t)v_sh |
+                          (uintptr_t)(quads ? v_sq : 0);
   IW_REQUIRE((align & 15) == 0, "decode attention operands must be 16-byte aligned");
   AttnArgs a;
   a.q = q;
@@ -162,6 +174,7 @@ int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k,
   a.v_sb = v_sb;
   a.v_sh = v_sh;
   a.v_sd = v_sd;
+  a.v_sq = v_sq;
   a.vt_ld = v_sd;
   a.out = out;
   a.o_sb = o_sb;
@@ -618,15 +631,17 @@ int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, i
 }
 
 int iw_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
-                       int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_offset,
+                       int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t dst_sq, int64_t t_offset,
                        int64_t batch, int64_t positions, int64_t heads, int64_t head_dim,
                        iw_stream_t stream) {
   IW_REQUIRE(batch >= 0 && positions >= 0 && heads > 0 && head_dim > 0 && t_offset >= 0,
              "invalid transpose shape");
+  IW_REQUIRE(dst_sq == 4 || (dst_sd == 4 && dst_sq >= 4 * head_dim),
+             "dst_sq == 4 (transposed rows) or dst_sd == 4 with dst_sq >= 4 * head_dim (key quads)");
   IW_REQUIRE(batch <= 65535, "batch too large for the transpose grid");
   if (batch * positions == 0) return IW_OK;
   IW_REQUIRE(src && dst, "null tensor pointer");
-  return launch_transpose_heads(src, src_sb, src_st, dst, dst_sb, dst_sh, dst_sd, t_offset, batch,
+  return launch_transpose_heads(src, src_sb, src_st, dst, dst_sb, dst_sh, dst_sd, dst_sq, t_offset, batch,
                                 positions, heads, head_dim, as_stream(stream));
 }
 
@@ -660,13 +675,13 @@ int iw_linear8_qkv_cache(const int8_t *x, const int8_t *weight, const int32_t *b
                          const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
                          int64_t M, int64_t K, bool has_bias, bool asymmetric, int8_t *q_out,
                          int64_t q_ld, int8_t *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
-                         int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
-                         int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
-                         const int32_t *pos, iw_stream_t stream) {
+                         int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t v_sq,
+                         int64_t channels, int64_t head_dim, int64_t tokens_per_row_group,
+                         int64_t cache_positions, const int32_t *pos, iw_stream_t stream) {
   GemmArgs g;
   SkinnyScatter sc;
   int rc = qkv_cache_args(x, weight, bias, weight_zero, multiplier, shift, M, K, has_bias, asymmetric, q_out,
-                          q_ld, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_sd, channels, head_dim,
+                          q_ld, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_sd, v_sq, channels, head_dim,
                           tokens_per_row_group, cache_positions, pos, &g, &sc);
   if (rc || M == 0) return rc;
   IW_REQUIRE(gemm_skinny_eligible(g), "QKV projection needs K % 16 == 0 and 16-byte aligned operands");
@@ -675,12 +690,13 @@ int iw_linear8_qkv_cache(const int8_t *x, const int8_t *weight, const int32_t *b
 
 int iw_attention_decode_cache(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
                               int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
-                              int64_t v_sh, int64_t v_sd, int8_t *out, int64_t o_sb, int64_t batch,
-                              int64_t heads, int64_t head_dim, int64_t k_length,
+                              int64_t v_sh, int64_t v_sd, int64_t v_sq, int8_t *out, int64_t o_sb,
+                              int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
                               const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                               int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
                               int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream) {
-  return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, out, o_sb, batch, heads,
+  return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, v_sq, out, o_sb, batch,
+                                      heads,
                                       head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
                                       av_multiplier, av_shift, rsqrt_offset, false, stream);
 }
@@ -905,13 +921,13 @@ int iw_linear8_qkv_cache_frag(const int8_t *x, const int8_t *weight, const int32
                               const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
                               int64_t M, int64_t K, bool has_bias, bool asymmetric, int8_t *q_out, int64_t q_ld,
                               int8_t *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st, int8_t *v_cache,
-                              int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels, int64_t head_dim,
-                              int64_t tokens_per_row_group, int64_t cache_positions, const int32_t *pos,
-                              iw_stream_t stream) {
+                              int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t v_sq, int64_t channels,
+                              int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
+                              const int32_t *pos, iw_stream_t stream) {
   GemmArgs g;
   SkinnyScatter sc;
   int rc = qkv_cache_args(x, weight, bias, weight_zero, multiplier, shift, M, K, has_bias, asymmetric, q_out,
-                          q_ld, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_sd, channels, head_dim,
+                          q_ld, k_cache, k_sb, k_sh, k_st, v_cache, v_sb, v_sh, v_sd, v_sq, channels, head_dim,
                           tokens_per_row_group, cache_positions, pos, &g, &sc);
   if (rc || M == 0) return rc;
   rc = check_frag(x, weight, M, K, 3 * channels);
@@ -932,11 +948,12 @@ int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *b
 
 int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb, int64_t k_sh,
                                    int64_t k_st, const int8_t *vt, int64_t v_sb, int64_t v_sh, int64_t v_sd,
-                                   int8_t *out, int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
-                                   const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier, int8_t qk_shift,
-                                   int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
+                                   int64_t v_sq, int8_t *out, int64_t batch, int64_t heads, int64_t head_dim,
+                                   int64_t k_length, const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
+                                   int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
                                    uint32_t rsqrt_offset, iw_stream_t stream) {
-  return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, out, 0, batch, heads,
+  return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, v_sq, out, 0, batch,
+                                      heads,
                                       head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
                                       av_multiplier, av_shift, rsqrt_offset, true, stream);
 }

@@ -783,6 +783,12 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 // waits for its own copies (vmcnt) and the ring needs no barrier. Keys past
 // Tk read the last valid key / piece; their scores are dropped and their P
 // is 0.
+//
+// VQ: V in key quads ([t/4][d][t%4], a quad of keys v_sq bytes apart). A
+// chunk of V is then CH/4 whole quads; a copy brings 4 quads, lane l the 16
+// bytes of d = 4 (l % 16) .. +3 of one quad, and the lane's four sdot4 take
+// the same P word. Each wave sums its own quads, so the d sums of the NW
+// waves meet in LDS at the end.
 // ---------------------------------------------------------------------------
 
 template <int N>
@@ -844,7 +850,7 @@ __device__ __forceinline__ void lds_barrier() {
 #define IW_DSS_NW 4
 #endif
 
-template <int MAXK, int NR, int CH, int NW = 4>
+template <int MAXK, int NR, int CH, int NW = 4, bool VQ = false>
 __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
   constexpr int D = 64;
   constexpr int DPC = CH / (16 * NW);  // copies per wave per chunk
@@ -853,8 +859,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   constexpr int WB = 1024 * DPC;      // bytes per wave per slot
   constexpr int LPR = CH / 16;        // lanes per V^T row piece set
   constexpr int RPD = 64 / LPR;       // V^T rows per copy
+  constexpr int NACC = VQ ? 4 : DPC;  // P.V sums per lane
+  static_assert(!VQ || NW * 64 * 4 <= MAXK * 2, "the wave sums of P.V fit in the score array");
   __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
-  __shared__ int16_t sS[MAXK];  // requantized scores
+  __shared__ __attribute__((aligned(16))) int16_t sS[MAXK];  // requantized scores
   __shared__ __attribute__((aligned(16))) uint8_t sP[MAXK];
   __shared__ int32_t sRed[NW];
   __shared__ uint32_t sSum[NW];
@@ -879,6 +887,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   const int vrow = wave * (64 / NW) + lane / LPR;
   const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (int64_t)vrow * a.v_sd;
   const int vlast = Tk > 0 ? ((Tk - 1) & ~15) : 0;  // last V^T piece holding a valid key
+  // V in key quads: copy u brings quad vq0 + 4 u of the chunk, d = 4 (l % 16) .. +3
+  const int vq0 = wave * DPC * 4 + (lane >> 4);
+  const int8_t *vqb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh + (lane & 15) * 16;
+  const int qlast = Tk > 0 ? (Tk - 1) >> 2 : 0;  // last quad holding a valid key
   const uint32_t ring =
       __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(sRing)) + wave * WB;
   auto issue = [&](int i) {
@@ -887,6 +899,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
 #pragma unroll
       for (int u = 0; u < DPC; ++u)
         dma16_lds(kb + (int64_t)min(i * CH + kkey + 16 * u, Tk - 1) * a.k_st, dst + u * 1024);
+    } else if (VQ) {
+#pragma unroll
+      for (int u = 0; u < DPC; ++u)
+        dma16_lds(vqb + (int64_t)min((i - nK) * (CH / 4) + vq0 + 4 * u, qlast) * a.v_sq, dst + u * 1024);
     } else {
 #pragma unroll
       for (int u = 0; u < DPC; ++u)
@@ -905,12 +921,12 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
     if (i < T) issue(i);
 
   int32_t mx = -32768;
-  uint32_t accd[DPC];
+  uint32_t accd[NACC];
 #pragma unroll
-  for (int u = 0; u < DPC; ++u) accd[u] = 0;
-  int32_t hs[DPC];
+  for (int u = 0; u < NACC; ++u) accd[u] = 0;
+  int32_t hs[NACC];
 #pragma unroll
-  for (int u = 0; u < DPC; ++u) hs[u] = 0;
+  for (int u = 0; u < NACC; ++u) hs[u] = 0;
   int32_t inv = 0;
   bool any_hi = false;
   v4i qv = v4i{0, 0, 0, 0};
@@ -979,6 +995,22 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
         }
       }
       if (i == nK - 1) form_p();
+    } else if (VQ) {
+#pragma unroll
+      for (int u = 0; u < DPC; ++u) {
+        const uint32_t pw = *reinterpret_cast<const uint32_t *>(sP + (i - nK) * CH + (vq0 + 4 * u) * 4);
+        if (!any_hi) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) accd[j] = (uint32_t)__builtin_amdgcn_sdot4((int)pw, x[u][j], (int)accd[j], false);
+        } else {
+          // P = 128 only after an int16 row-max wrap: split off the top bit
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            accd[j] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw & 0x7f7f7f7fu), x[u][j], (int)accd[j], false);
+            hs[j] = __builtin_amdgcn_sdot4((int)((pw >> 7) & 0x01010101u), x[u][j], hs[j], false);
+          }
+        }
+      }
     } else {
       const uint4 pv = *reinterpret_cast<const uint4 *>(sP + (i - nK) * CH + vp * 16);
       const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
@@ -999,16 +1031,39 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
       }
     }
   }
+  auto store = [&](uint32_t v, int d) {
+    int32_t y = rshift((int32_t)(v * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+    a.out[decode_out_index(a, b, h * D + d)] = (int8_t)clampi(y, -127, 127);
+  };
+  if (VQ) {
+    // lanes l and l ^ 16, l ^ 32 hold other quads of the same d; then the
+    // waves' sums meet in sS, free since form_p's last barrier
+    uint4 v;
+    uint32_t *vw = &v.x;
 #pragma unroll
-  for (int u = 0; u < DPC; ++u) {
-    uint32_t v = accd[u] + ((uint32_t)hs[u] << 7);
+    for (int j = 0; j < 4; ++j) {
+      uint32_t t = accd[j] + ((uint32_t)hs[j] << 7);
+      t += (uint32_t)__shfl_xor((int)t, 16);
+      vw[j] = t + (uint32_t)__shfl_xor((int)t, 32);
+    }
+    uint32_t *sPart = reinterpret_cast<uint32_t *>(sS);
+    if (lane < 16) *reinterpret_cast<uint4 *>(sPart + wave * 64 + 4 * lane) = v;
+    lds_barrier();
+    if (tid < 64) {
+      uint32_t t = 0;
 #pragma unroll
-    for (int o = 1; o < LPR; o <<= 1) v += (uint32_t)__shfl_xor((int)v, o);
-    if (vp == 0) {
-      int32_t y = rshift((int32_t)(v * (uint32_t)inv), a.rsqrt_off);
-      y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
-      y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
-      a.out[decode_out_index(a, b, h * D + vrow + u * RPD)] = (int8_t)clampi(y, -127, 127);
+      for (int w = 0; w < NW; ++w) t += sPart[w * 64 + tid];
+      store(t, tid);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < DPC; ++u) {
+      uint32_t v = accd[u] + ((uint32_t)hs[u] << 7);
+#pragma unroll
+      for (int o = 1; o < LPR; o <<= 1) v += (uint32_t)__shfl_xor((int)v, o);
+      if (vp == 0) store(v, vrow + u * RPD);
     }
   }
 }
@@ -1081,23 +1136,33 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
   const int sets = ((a.max_tk + 15) / 16 + 63) / 64;
   const dim3 grid((unsigned)(a.B * a.H));
   // head_dim 64 with 16-byte key rows and V^T rows: the streaming kernel
+  const bool vq = a.v_sq != 4;  // V in key quads
   const uintptr_t al = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.vt) |
                        reinterpret_cast<uintptr_t>(a.q) | (uintptr_t)a.k_st | (uintptr_t)a.k_sh |
-                       (uintptr_t)a.k_sb | (uintptr_t)a.v_sd | (uintptr_t)a.v_sh | (uintptr_t)a.v_sb |
-                       (uintptr_t)a.q_sb;
+                       (uintptr_t)a.k_sb | (uintptr_t)(vq ? a.v_sq : a.v_sd) | (uintptr_t)a.v_sh |
+                       (uintptr_t)a.v_sb | (uintptr_t)a.q_sb;
   if (a.D == 64 && (al & 15) == 0 && a.max_tk <= DC_MAX_TK) {
     // (self-attention caches up to 512 positions get their own, smaller
     // instance, so profiles separate it from cross-attention)
-    if (a.max_tk <= 512)
-      hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DSS_NR, IW_DSS_CH, IW_DSS_NW>), grid, dim3(64 * IW_DSS_NW),
-                         0, s, a, pos);
-    else if (a.max_tk <= 2048)
-      hipLaunchKernelGGL((attn_decode_stream_kernel<2048, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a, pos);
-    else
-      hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, IW_DS_NR, IW_DS_CH>), grid, dim3(256), 0, s, a,
-                         pos);
+#define IW_DS(VQ_)                                                                                             \
+  if (a.max_tk <= 512)                                                                                         \
+    hipLaunchKernelGGL((attn_decode_stream_kernel<512, IW_DSS_NR, IW_DSS_CH, IW_DSS_NW, VQ_>), grid,            \
+                       dim3(64 * IW_DSS_NW), 0, s, a, pos);                                                    \
+  else if (a.max_tk <= 2048)                                                                                   \
+    hipLaunchKernelGGL((attn_decode_stream_kernel<2048, IW_DS_NR, IW_DS_CH, 4, VQ_>), grid, dim3(256), 0, s, a, \
+                       pos);                                                                                   \
+  else                                                                                                         \
+    hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, IW_DS_NR, IW_DS_CH, 4, VQ_>), grid, dim3(256), 0, \
+                       s, a, pos);
+    if (vq) {
+      IW_DS(true)
+    } else {
+      IW_DS(false)
+    }
+#undef IW_DS
     return check_launch("attn_decode_stream_kernel");
   }
+  if (vq) return fail("V in key quads needs head_dim 64 and 16-byte aligned operands");
 #define IW_DC(D_, P_) hipLaunchKernelGGL((attn_decode_cache_kernel<D_, P_>), grid, dim3(256), 0, s, a, pos)
   switch (a.D) {
     case 64:

@@ -85,14 +85,16 @@ struct GemmArgs {
 // Decode-step QKV projection: the epilogue writes Q (columns [0, C)) to
 // q[m][n], and appends K / V (columns [C, 2C) / [2C, 3C), head h = c / D,
 // d = c % D) of row m = b * T + i at cache position t = *pos + i:
-// K to k[b*k_sb + h*k_sh + t*k_st + d], V to v[b*v_sb + h*v_sh + d*v_sd + t].
+// K to k[b*k_sb + h*k_sh + t*k_st + d], V to
+// v[b*v_sb + h*v_sh + d*v_sd + (t/4)*v_sq + t%4] (v_sq = 4: V transposed per
+// head; v_sd = 4, v_sq = 4 D: key quads, one step's V of a head in 4 D bytes).
 struct SkinnyScatter {
   int8_t *q = nullptr;
   int64_t ldq = 0;
   int8_t *k = nullptr;
   int64_t k_sb = 0, k_sh = 0, k_st = 0;
   int8_t *v = nullptr;
-  int64_t v_sb = 0, v_sh = 0, v_sd = 0;
+  int64_t v_sb = 0, v_sh = 0, v_sd = 0, v_sq = 4;
   int C = 0, D = 1, T = 1;
   int t_cap = 0;  // cache positions; appends at t >= t_cap are dropped
   const int32_t *pos = nullptr;

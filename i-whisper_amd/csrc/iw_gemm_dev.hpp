@@ -252,8 +252,9 @@ __device__ __forceinline__ void skinny_store(const GemmArgs &g, const SkinnyScat
     if (GELU) y = gelu_dec(y, lut, c);
     if (SCATTER) {
       // columns [0, C): Q; [C, 2C): K appended at position pos + (m % T)
-      // of the [B, H, T_cache, D] cache; [2C, 3C): V appended to the
-      // transposed [B, H, D, T_cache] cache
+      // of the [B, H, T_cache, D] cache; [2C, 3C): V appended to the V
+      // cache, transposed [B, H, D, T_cache] or in key quads
+      // [B, H, T_cache / 4, D, 4]
       const int b = m / sc.T, t = pos + m % sc.T;
       if (n < sc.C) {
         sc.q[(int64_t)m * sc.ldq + n] = (int8_t)y;
@@ -264,7 +265,8 @@ __device__ __forceinline__ void skinny_store(const GemmArgs &g, const SkinnyScat
         sc.k[(int64_t)b * sc.k_sb + (int64_t)h * sc.k_sh + (int64_t)t * sc.k_st + d] = (int8_t)y;
       } else {
         const int h = (n - 2 * sc.C) / sc.D, d = (n - 2 * sc.C) % sc.D;
-        sc.v[(int64_t)b * sc.v_sb + (int64_t)h * sc.v_sh + (int64_t)d * sc.v_sd + t] = (int8_t)y;
+        sc.v[(int64_t)b * sc.v_sb + (int64_t)h * sc.v_sh + (int64_t)d * sc.v_sd + (int64_t)(t >> 2) * sc.v_sq +
+             (t & 3)] = (int8_t)y;
       }
     } else if (OUT_FRAG) {
       // fragment-major output: g.ldc is its padded K

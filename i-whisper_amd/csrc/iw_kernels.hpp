@@ -14,7 +14,9 @@ struct FragPrefetch;  // iw_gemm.hpp
 // Fused attention arguments. Element (b, t, h, d) of a [B, T, H*D] operand
 // lives at base + b * sb + t * st + h * D + d. V is given transposed per
 // head: vt + b * v_sb + h * v_sh + d * v_sd + t (prefill: v_sh = D * vt_ld,
-// v_sd = vt_ld, v_sb = H * D * vt_ld).
+// v_sd = vt_ld, v_sb = H * D * vt_ld); the decode kernels over caches also
+// take it in key quads (v_sq != 4, v_sd = 4): vt + b * v_sb + h * v_sh +
+// (t / 4) * v_sq + 4 d + t % 4.
 struct AttnArgs {
   const int8_t *q = nullptr;
   int64_t q_sb = 0, q_st = 0;
@@ -22,6 +24,7 @@ struct AttnArgs {
   int64_t k_sb = 0, k_sh = 0, k_st = 0;  // decode: explicit per-head stride
   const int8_t *vt = nullptr;
   int64_t v_sb = 0, v_sh = 0, v_sd = 0, vt_ld = 0;
+  int64_t v_sq = 4;  // key-quad stride; 4 = transposed rows
   int8_t *out = nullptr;
   int64_t o_sb = 0, o_st = 0;
   const uint8_t *mask = nullptr;  // [Tq][Tk] bool bytes, or null
@@ -85,8 +88,9 @@ int launch_token_prob(const int8_t *logits, int64_t rows, int64_t cols, int64_t 
                       float *out, hipStream_t s);
 int launch_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int64_t *out,
                        hipStream_t s);
+// dst[b*dst_sb + h*dst_sh + d*dst_sd + (t/4)*dst_sq + t%4] for t = t_off + i
 int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
-                           int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off,
+                           int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t dst_sq, int64_t t_off,
                            int64_t B, int64_t T, int64_t H, int64_t D, hipStream_t s);
 int launch_gather_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
                         int64_t dst_sb, int64_t dst_sh, int64_t dst_st, int64_t t_off, int64_t B,

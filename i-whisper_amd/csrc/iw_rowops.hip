@@ -921,13 +921,14 @@ __global__ void greedy_advance_kernel(int32_t *step, int32_t *pos, int32_t pos_i
   }
 }
 
-// Per-head transpose of a [B, T, H*D] operand slice into V^T layout:
-// dst[b][h][d][t_off + t] = src[b*src_sb + t*src_st + h*D + d].
+// Per-head transpose of a [B, T, H*D] operand slice into a V cache: with
+// p = t_off + t, dst[b*dst_sb + h*dst_sh + d*dst_sd + (p/4)*dst_sq + p%4] =
+// src[b*src_sb + t*src_st + h*D + d] (dst_sq = 4: V^T rows [b][h][d][p]).
 // Tiles of 64 positions x 64 feature columns go through LDS so that both the
-// reads (along features) and the writes (along positions) are contiguous.
+// reads (along features) and the V^T writes (along positions) are contiguous.
 __global__ __launch_bounds__(256) void transpose_heads_kernel(
     const int8_t *__restrict__ src, int64_t src_sb, int64_t src_st, int8_t *__restrict__ dst,
-    int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off, int64_t T, int64_t H,
+    int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t dst_sq, int64_t t_off, int64_t T, int64_t H,
     int64_t D) {
   __shared__ int8_t tile[64][65];
   const int64_t b = blockIdx.z;
@@ -944,7 +945,8 @@ __global__ __launch_bounds__(256) void transpose_heads_kernel(
     const int64_t c = c0 + r, t = t0 + tx;
     if (t < T && c < C) {
       const int64_t h = c / D, d = c % D;
-      dst[b * dst_sb + h * dst_sh + d * dst_sd + t_off + t] = tile[tx][r];
+      const int64_t p = t_off + t;  // cache position
+      dst[b * dst_sb + h * dst_sh + d * dst_sd + (p >> 2) * dst_sq + (p & 3)] = tile[tx][r];
     }
   }
 }
@@ -1143,20 +1145,20 @@ int launch_quantize_mel(const float *mel, float alpha, int8_t *out, int64_t b, i
 }
 
 int launch_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
-                           int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_off,
+                           int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t dst_sq, int64_t t_off,
                            int64_t B, int64_t T, int64_t H, int64_t D, hipStream_t s) {
   if (B * T * H * D == 0) return 0;
   const dim3 grid((unsigned)((T + 63) / 64), (unsigned)((H * D + 63) / 64), (unsigned)B);
   const uintptr_t al = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | (uintptr_t)src_sb |
                        (uintptr_t)src_st | (uintptr_t)dst_sb | (uintptr_t)dst_sh | (uintptr_t)dst_sd |
                        (uintptr_t)t_off | (uintptr_t)(H * D);
-  if ((al & 15) == 0 && H * D <= 0x7fffffff) {
+  if (dst_sq == 4 && (al & 15) == 0 && H * D <= 0x7fffffff) {
     hipLaunchKernelGGL(transpose_heads16_kernel, grid, dim3(256), 0, s, src, src_sb, src_st, dst, dst_sb, dst_sh,
                        dst_sd, t_off, T, H, D);
     return check_launch("transpose_heads16_kernel");
   }
   hipLaunchKernelGGL(transpose_heads_kernel, grid, dim3(256), 0, s, src, src_sb, src_st, dst,
-                     dst_sb, dst_sh, dst_sd, t_off, T, H, D);
+                     dst_sb, dst_sh, dst_sd, dst_sq, t_off, T, H, D);
   return check_launch("transpose_heads_kernel");
 }
 

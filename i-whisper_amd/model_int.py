@@ -266,7 +266,7 @@ def pack_vt(v: Tensor, n_head: int, pad_to: int = 16) -> Tensor:
     tp = (Tk + pad_to - 1) // pad_to * pad_to
     vt = torch.empty((B, n_head, D, tp), dtype=torch.int8, device=v.device)
     _lib.call("iw_transpose_heads", v.data_ptr(), v.stride(0), v.stride(1), vt.data_ptr(),
-              n_head * D * tp, D * tp, tp, 0, B, Tk, n_head, D, _stream())
+              n_head * D * tp, D * tp, tp, 4, 0, B, Tk, n_head, D, _stream())
     return vt
 
 

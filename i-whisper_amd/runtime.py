@@ -232,7 +232,7 @@ class EncoderRunner:
         self._tock(t)
         q = self.qkv_buf.data_ptr()
         _lib.call("iw_transpose_heads", q + 2 * C, T * 3 * C, 3 * C, self.vt.data_ptr(),
-                  H * D * self.tp, D * self.tp, self.tp, 0, B, T, H, D, _stream())
+                  H * D * self.tp, D * self.tp, self.tp, 4, 0, B, T, H, D, _stream())
         t = self._tick("attention", 4.0 * B * H * T * T * D)
         _lib.call("iw_attention", q, T * 3 * C, 3 * C, q + C, T * 3 * C, D, 3 * C,
                   self.vt.data_ptr(), H * D * self.tp, D * self.tp, self.tp, self.wv.data_ptr(),
@@ -332,7 +332,16 @@ class DecoderRunner:
         self.self_qkv = [_FusedLinear([b.attn.query, b.attn.key, b.attn.value]) for b in decoder.blocks]
         self.cross_kv = [_FusedLinear([b.cross_attn.key, b.cross_attn.value]) for b in decoder.blocks]
         self.k_self = [torch.zeros((batch, H, self.Tcap, D), **i8) for _ in range(L)]
-        self.vt_self = [torch.zeros((batch, H, D, self.tcap16), **i8) for _ in range(L)]
+        # V of the self-attention in key quads [B, H, Tcap/4, D, 4] (one
+        # token's append is 4 D contiguous bytes per head) where the decode
+        # attention reads them (head_dim 64), else transposed [B, H, D, Tcap]
+        self.v_quads = D == 64
+        if self.v_quads:
+            self.v_self = [torch.zeros((batch, H, self.tcap16 // 4, 4 * D), **i8) for _ in range(L)]
+            self.v_strides = (H * self.tcap16 * D, self.tcap16 * D, 4, 4 * D)
+        else:
+            self.v_self = [torch.zeros((batch, H, D, self.tcap16), **i8) for _ in range(L)]
+            self.v_strides = (H * D * self.tcap16, D * self.tcap16, self.tcap16, 4)
         self.k_cross = [torch.zeros((batch, H, n_audio_ctx, D), **i8) for _ in range(L)]
         self.vt_cross = [torch.zeros((batch, H, D, self.ta16), **i8) for _ in range(L)]
         self.kv_tmp = torch.empty((batch * n_audio_ctx, 2 * C), **i8)
@@ -422,7 +431,7 @@ class DecoderRunner:
             _lib.call("iw_gather_heads", kv.data_ptr(), Ta * 2 * C, 2 * C, self.k_cross[l].data_ptr(),
                       H * Ta * D, Ta * D, D, 0, B, Ta, H, D, _stream())
             _lib.call("iw_transpose_heads", kv.data_ptr() + C, Ta * 2 * C, 2 * C,
-                      self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16, 0, B,
+                      self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16, 4, 0, B,
                       Ta, H, D, _stream())
 
     def reset(self):
@@ -443,7 +452,7 @@ class DecoderRunner:
             for i in range(Tq):
                 _lib.call("iw_attention_decode_cache", q_ptr + i * q_st, q_sb, self.k_cross[l].data_ptr(),
                           H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
-                          D * self.ta16, self.ta16, out.data_ptr() + i * self.C, Tq * self.C, self.B, H, D,
+                          D * self.ta16, self.ta16, 4, out.data_ptr() + i * self.C, Tq * self.C, self.B, H, D,
                           Ta, None, Ta, s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset,
                           _stream())
         else:
@@ -515,6 +524,10 @@ class DecoderRunner:
         qc = torch.empty((M, C), dtype=torch.int8, device=dev)
         f8 = torch.empty((M, 4 * C), dtype=torch.int8, device=dev)
         mask = dec.mask[:P, :P].contiguous()
+        # the prompt's V transposed for the prefill attention (the cache may
+        # hold key quads)
+        p16 = (P + 15) // 16 * 16
+        vt = torch.empty((B, H, D, p16), dtype=torch.int8, device=dev) if self.v_quads else None
         for l, blk in enumerate(dec.blocks):
             sc = blk._scalars()
             _ln(blk.attn_ln, x16, M, h8)
@@ -522,12 +535,17 @@ class DecoderRunner:
             q = qkv.data_ptr()
             _lib.call("iw_gather_heads", q + C, P * 3 * C, 3 * C, self.k_self[l].data_ptr(),
                       H * self.Tcap * D, self.Tcap * D, D, 0, B, P, H, D, _stream())
-            _lib.call("iw_transpose_heads", q + 2 * C, P * 3 * C, 3 * C, self.vt_self[l].data_ptr(),
-                      H * D * self.tcap16, D * self.tcap16, self.tcap16, 0, B, P, H, D, _stream())
+            _lib.call("iw_transpose_heads", q + 2 * C, P * 3 * C, 3 * C, self.v_self[l].data_ptr(),
+                      *self.v_strides, 0, B, P, H, D, _stream())
+            if vt is not None:
+                _lib.call("iw_transpose_heads", q + 2 * C, P * 3 * C, 3 * C, vt.data_ptr(), H * D * p16,
+                          D * p16, p16, 4, 0, B, P, H, D, _stream())
+                vt_args = (vt.data_ptr(), H * D * p16, D * p16, p16)
+            else:
+                vt_args = (self.v_self[l].data_ptr(), *self.v_strides[:3])
             s = blk.attn._scalars()
             _lib.call("iw_attention", q, P * 3 * C, 3 * C, self.k_self[l].data_ptr(), H * self.Tcap * D,
-                      self.Tcap * D, D, self.vt_self[l].data_ptr(), H * D * self.tcap16,
-                      D * self.tcap16, self.tcap16, wv.data_ptr(), P * C, C, mask.data_ptr(), B, H, P,
+                      self.Tcap * D, D, *vt_args, wv.data_ptr(), P * C, C, mask.data_ptr(), B, H, P,
                       P, D, s["qm"], s["qs"], s["f"], s["am"], s["as_"], blk.attn.rsqrt_offset,
                       self.self_tables[l].data_ptr(), False, _stream())
             _lin32_res(blk.attn.out, wv.data_ptr(), M, x16, sc["a"])
@@ -573,12 +591,12 @@ class DecoderRunner:
             _lib.call("iw_linear8_qkv_cache", h8.data_ptr(), fq.weight.data_ptr(), fq.bias.data_ptr(),
                       fq.wz.data_ptr(), fq.mult.data_ptr(), fq.shift.data_ptr(), B, C, True, True,
                       q8.data_ptr(), C, self.k_self[l].data_ptr(), H * self.Tcap * D, self.Tcap * D, D,
-                      self.vt_self[l].data_ptr(), H * D * self.tcap16, D * self.tcap16, self.tcap16, C,
-                      D, 1, self.Tcap, self.pos.data_ptr(), _stream())
+                      self.v_self[l].data_ptr(), *self.v_strides, C, D, 1, self.Tcap, self.pos.data_ptr(),
+                      _stream())
             s = blk.attn._scalars()
             _lib.call("iw_attention_decode_cache", q8.data_ptr(), C, self.k_self[l].data_ptr(),
-                      H * self.Tcap * D, self.Tcap * D, D, self.vt_self[l].data_ptr(),
-                      H * D * self.tcap16, D * self.tcap16, self.tcap16, wv.data_ptr(), C, B, H, D, 1,
+                      H * self.Tcap * D, self.Tcap * D, D, self.v_self[l].data_ptr(), *self.v_strides,
+                      wv.data_ptr(), C, B, H, D, 1,
                       self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
                       blk.attn.rsqrt_offset, _stream())
             _lin32_res(blk.attn.out, wv.data_ptr(), B, x16, sc["a"])
@@ -604,12 +622,12 @@ class DecoderRunner:
             _ln_frag(blk.attn_ln, x16, B, h8f, pf(fq))
             _lib.call("iw_linear8_qkv_cache_frag", h8f.data_ptr(), *fq.args(), B, C, True, True,
                       q8.data_ptr(), C, self.k_self[l].data_ptr(), H * self.Tcap * D, self.Tcap * D, D,
-                      self.vt_self[l].data_ptr(), H * D * self.tcap16, D * self.tcap16, self.tcap16, C,
-                      D, 1, self.Tcap, self.pos.data_ptr(), _stream())
+                      self.v_self[l].data_ptr(), *self.v_strides, C, D, 1, self.Tcap, self.pos.data_ptr(),
+                      _stream())
             s = blk.attn._scalars()
             _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_self[l].data_ptr(),
-                      H * self.Tcap * D, self.Tcap * D, D, self.vt_self[l].data_ptr(),
-                      H * D * self.tcap16, D * self.tcap16, self.tcap16, wvf.data_ptr(), B, H, D, 1,
+                      H * self.Tcap * D, self.Tcap * D, D, self.v_self[l].data_ptr(), *self.v_strides,
+                      wvf.data_ptr(), B, H, D, 1,
                       self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
                       blk.attn.rsqrt_offset, _stream())
             self.f_out[l].linear32_res(wvf, B, x16, sc["a"])
@@ -619,7 +637,7 @@ class DecoderRunner:
             Ta = self.Ta
             _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_cross[l].data_ptr(),
                       H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
-                      D * self.ta16, self.ta16, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
+                      D * self.ta16, self.ta16, 4, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
                       s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
             self.f_co[l].linear32_res(wvf, B, x16, sc["c"])
             f1, f2 = self.f_fc1[l], self.f_fc2[l]

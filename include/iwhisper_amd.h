@@ -220,13 +220,15 @@ int iw_attention(const int8_t *q, int64_t q_sb, int64_t q_st, const int8_t *k, i
 
 /* Layout helpers for the KV caches (the reference's view/permute/.contiguous()
  * copies and hook-side torch.cat, model_int.py:842-949 and 1604-1610):
- * transpose_heads writes dst[b][h][d][t_offset+t] = src[b*src_sb + t*src_st + h*D + d]
- * (V^T per head); copy_rows writes dst[b*dst_sb + (t_offset+t)*dst_st + c] =
- * src[b*src_sb + t*src_st + c] for c < channels. */
+ * transpose_heads writes, with p = t_offset + t,
+ * dst[b*dst_sb + h*dst_sh + d*dst_sd + (p/4)*dst_sq + p%4] = src[b*src_sb + t*src_st + h*D + d]
+ * (dst_sq = 4: V^T per head, dst[b][h][d][p]; dst_sd = 4, dst_sq >= 4*head_dim:
+ * V in key quads, see the decode step below); copy_rows writes
+ * dst[b*dst_sb + (t_offset+t)*dst_st + c] = src[b*src_sb + t*src_st + c] for c < channels. */
 int iw_transpose_heads(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst,
-                       int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t t_offset,
-                       int64_t batch, int64_t positions, int64_t heads, int64_t head_dim,
-                       iw_stream_t stream);
+                       int64_t dst_sb, int64_t dst_sh, int64_t dst_sd, int64_t dst_sq,
+                       int64_t t_offset, int64_t batch, int64_t positions, int64_t heads,
+                       int64_t head_dim, iw_stream_t stream);
 int iw_copy_rows(const int8_t *src, int64_t src_sb, int64_t src_st, int8_t *dst, int64_t dst_sb,
                  int64_t dst_st, int64_t t_offset, int64_t batch, int64_t positions,
                  int64_t channels, iw_stream_t stream);
@@ -245,8 +247,13 @@ int iw_argmax_rows(const int8_t *x, int64_t rows, int64_t cols, int64_t ld, int6
  * of the self-attention K/V (model_int.py:1587-1618), the cross-attention
  * K/V reuse (model_int.py:722-730) and GreedyDecoder.update
  * (decoding.py:280-296). Cache layouts: K [b][h][t][d] at
- * k + b*k_sb + h*k_sh + t*k_st + d; V transposed per head [b][h][d][t] at
- * v + b*v_sb + h*v_sh + d*v_sd + t.
+ * k + b*k_sb + h*k_sh + t*k_st + d; V at v + b*v_sb + h*v_sh + d*v_sd + (t/4)*v_sq + t%4,
+ * in one of two forms:
+ *   transposed per head [b][h][d][t]: v_sq = 4, row d of a head at d*v_sd;
+ *   key quads [b][h][t/4][d][t%4]: v_sd = 4, v_sq >= 4*head_dim (v_sq = 4*head_dim
+ *   packs them): one token's V of a head is 4*head_dim bytes of one quad, so
+ *   the per-step append touches 4 cache lines per head instead of head_dim.
+ * The decode attention reads key quads for head_dim 64 (v_sq % 16 == 0).
  * ------------------------------------------------------------------------- */
 
 /* Self-attention Q/K/V projection (MultiHeadAttention_int.forward,
@@ -258,18 +265,19 @@ int iw_linear8_qkv_cache(const int8_t *x, const int8_t *weight, const int32_t *b
                          const int8_t *weight_zero, const uint32_t *multiplier, const int8_t *shift,
                          int64_t M, int64_t K, bool has_bias, bool asymmetric, int8_t *q_out,
                          int64_t q_ld, int8_t *k_cache, int64_t k_sb, int64_t k_sh, int64_t k_st,
-                         int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
-                         int64_t head_dim, int64_t tokens_per_row_group, int64_t cache_positions,
-                         const int32_t *pos, iw_stream_t stream);
+                         int8_t *v_cache, int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t v_sq,
+                         int64_t channels, int64_t head_dim, int64_t tokens_per_row_group,
+                         int64_t cache_positions, const int32_t *pos, iw_stream_t stream);
 
 /* One-query attention over the caches (qkv_attention for q_length 1,
  * model_int.py:774-1040): q [b][h*D] at q + b*q_sb, out at out + b*o_sb.
  * The key count is min(k_length + *pos, max_keys) (pos may be NULL when
- * max_keys == k_length); max_keys <= 4096, v_sd covers round_up(max_keys, 16). */
+ * max_keys == k_length); max_keys <= 4096; transposed V rows (v_sq = 4) hold
+ * round_up(max_keys, 16) bytes, key quads cover round_up(max_keys, 4) keys. */
 int iw_attention_decode_cache(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
                               int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
-                              int64_t v_sh, int64_t v_sd, int8_t *out, int64_t o_sb, int64_t batch,
-                              int64_t heads, int64_t head_dim, int64_t k_length,
+                              int64_t v_sh, int64_t v_sd, int64_t v_sq, int8_t *out, int64_t o_sb,
+                              int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
                               const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                               int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
                               int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream);
@@ -379,8 +387,8 @@ int iw_linear8_qkv_cache_frag(const int8_t *x, const int8_t *weight, const int32
                               const int8_t *shift, int64_t M, int64_t K, bool has_bias,
                               bool asymmetric, int8_t *q_out, int64_t q_ld, int8_t *k_cache,
                               int64_t k_sb, int64_t k_sh, int64_t k_st, int8_t *v_cache,
-                              int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t channels,
-                              int64_t head_dim, int64_t tokens_per_row_group,
+                              int64_t v_sb, int64_t v_sh, int64_t v_sd, int64_t v_sq,
+                              int64_t channels, int64_t head_dim, int64_t tokens_per_row_group,
                               int64_t cache_positions, const int32_t *pos, iw_stream_t stream);
 
 /* iw_layernorm32 writing the fragment-major image of out [rows][hidden]
@@ -396,8 +404,8 @@ int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *b
  * [batch][heads*head_dim] (batch <= 128, heads*head_dim <= 5120). */
 int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
                                    int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
-                                   int64_t v_sh, int64_t v_sd, int8_t *out, int64_t batch,
-                                   int64_t heads, int64_t head_dim, int64_t k_length,
+                                   int64_t v_sh, int64_t v_sd, int64_t v_sq, int8_t *out,
+                                   int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
                                    const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                                    int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
                                    int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream);

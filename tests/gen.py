@@ -80,3 +80,32 @@ def causal_mask(tq, tk):
     off = tk - tq
     full = np.triu(np.ones((tk, tk), dtype=bool), 1)
     return np.ascontiguousarray(full[off:off + tq, :tk])
+
+
+# V caches of the decode entry points: element (b, h, t, d) at
+# b*v_sb + h*v_sh + d*v_sd + (t//4)*v_sq + t%4.
+V_LAYOUTS = ("vt", "quads", "quads_pad")
+
+
+def v_cache_layout(B, H, D, tcap, layout):
+    """Array shape and (v_sb, v_sh, v_sd, v_sq) of a V cache of tcap positions:
+    'vt' transposed rows [B, H, D, round_up(tcap, 16)]; 'quads' key quads
+    [B, H, round_up(tcap, 16) / 4, 4 D]; 'quads_pad' the same with 16 unused
+    bytes after each quad."""
+    tc16 = (tcap + 15) // 16 * 16
+    if layout == "vt":
+        return (B, H, D, tc16), (H * D * tc16, D * tc16, tc16, 4)
+    qs = 4 * D + (16 if layout == "quads_pad" else 0)
+    nq = tc16 // 4
+    return (B, H, nq, qs), (H * nq * qs, nq * qs, 4, qs)
+
+
+def v_cache_put(cache, layout, t0, vt):
+    """Write vt [B, H, D, n] (V transposed) at positions t0 .. t0 + n - 1."""
+    if layout == "vt":
+        cache[..., t0:t0 + vt.shape[-1]] = vt
+        return
+    D = vt.shape[2]
+    for i in range(vt.shape[-1]):
+        t = t0 + i
+        cache[:, :, t // 4, 4 * np.arange(D) + t % 4] = vt[..., i]

@@ -33,22 +33,23 @@ def stream():
     return torch.cuda.current_stream().cuda_stream
 
 
-def _decode_cache(iw, q, k, v, qm, qs, f, am, as_, *, tcap, k_length, pos_val, max_keys):
-    """q [B,H,1,D], k [B,H,Tk,D], v [B,H,D,Tk] placed in caches with random fill."""
+def _decode_cache(iw, q, k, v, qm, qs, f, am, as_, *, tcap, k_length, pos_val, max_keys, layout="vt"):
+    """q [B,H,1,D], k [B,H,Tk,D], v [B,H,D,Tk] placed in caches with random fill
+    (V in the given cache layout)."""
     B, H, _, D = q.shape
     Tk = k.shape[2]
     r = gen.rng(B + H + Tk)
-    tc16 = (tcap + 15) // 16 * 16
     kc = gen.i8(r, (B, H, tcap, D))
     kc[:, :, :Tk] = k
-    vc = gen.i8(r, (B, H, D, tc16))
-    vc[..., :Tk] = v
+    shape, vs = gen.v_cache_layout(B, H, D, tcap, layout)
+    vc = gen.i8(r, shape)
+    gen.v_cache_put(vc, layout, 0, v)
     qh = np.ascontiguousarray(q[:, :, 0, :].reshape(B, H * D))
     out = torch.empty((B, H * D), dtype=torch.int8, device="cuda")
     pos = None if pos_val is None else torch.tensor([pos_val], dtype=torch.int32, device="cuda")
     qt, kt, vt = T(qh), T(kc), T(vc)
     iw._lib.call("iw_attention_decode_cache", qt.data_ptr(), H * D, kt.data_ptr(), H * tcap * D,
-                 tcap * D, D, vt.data_ptr(), H * D * tc16, D * tc16, tc16, out.data_ptr(), H * D, B, H,
+                 tcap * D, D, vt.data_ptr(), *vs, out.data_ptr(), H * D, B, H,
                  D, k_length, None if pos is None else pos.data_ptr(), max_keys, qm, qs, f, am, as_, 16,
                  stream())
     return host(out).reshape(B, 1, H * D)
@@ -58,27 +59,63 @@ def _decode_cache(iw, q, k, v, qm, qs, f, am, as_, *, tcap, k_length, pos_val, m
     (2, 3, 64, 1, 448, 1), (2, 3, 64, 17, 448, 1), (1, 2, 64, 448, 448, 1), (3, 2, 64, 200, 448, 1),
     (2, 4, 64, 1500, 1500, 1500), (1, 2, 96, 100, 448, 1), (1, 1, 128, 300, 448, 1),
     (2, 2, 64, 33, 40, 33)])
-def test_attention_decode_cache(iw, oracle, gpu, B, H, D, Tk, tcap, k_length):
-    print("case: decode cache", B, H, D, Tk, tcap, k_length, flush=True)
+@pytest.mark.parametrize("layout", gen.V_LAYOUTS)
+def test_attention_decode_cache(iw, oracle, gpu, B, H, D, Tk, tcap, k_length, layout):
+    if layout != "vt" and D != 64:
+        pytest.skip("V in key quads is read for head_dim 64")
+    print("case: decode cache", B, H, D, Tk, tcap, k_length, layout, flush=True)
     q, k, v, qm, qs, f, am, as_ = gen.attn_case(3 * B + Tk + D, B, H, 1, Tk, D)
     exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
     pos_val = None if k_length == Tk else Tk - k_length
     got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=k_length,
-                        pos_val=pos_val, max_keys=tcap if pos_val is not None else k_length)
+                        pos_val=pos_val, max_keys=tcap if pos_val is not None else k_length, layout=layout)
     assert np.array_equal(got, exp)
 
 
-def test_attention_decode_cache_clamps_keys(iw, oracle, gpu):
+@pytest.mark.parametrize("Tk", [1, 2, 3, 4, 5, 127, 128, 129, 255, 257, 446, 447, 448])
+def test_attention_decode_cache_quads_ragged(iw, oracle, gpu, Tk):
+    """Key counts that end inside a quad, a 128-key chunk or the cache
+    (self-attention shapes: 20 heads, 448 positions, key count k_length + *pos)."""
+    print("case: decode cache quads ragged", Tk, flush=True)
+    B, H, D, tcap = 3, 20, 64, 448
+    q, k, v, qm, qs, f, am, as_ = gen.attn_case(31 * Tk + 5, B, H, 1, Tk, D)
+    exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
+    got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=1, pos_val=Tk - 1,
+                        max_keys=tcap, layout="quads")
+    assert np.array_equal(got, exp)
+
+
+def test_attention_decode_cache_quads_rejects(iw, gpu):
+    """Key quads need head_dim 64, v_sd 4 and a 16-byte multiple v_sq of at
+    least 4 head_dim."""
+    B, H, tcap = 1, 2, 64
+    q = torch.zeros((B, H * 96), dtype=torch.int8, device="cuda")
+    k = torch.zeros((B, H, tcap, 96), dtype=torch.int8, device="cuda")
+    v = torch.zeros(B * H * tcap * 96 + 4096, dtype=torch.int8, device="cuda")
+    out = torch.empty((B, H * 96), dtype=torch.int8, device="cuda")
+    for D, vs, what in ((96, (H * tcap * 96, tcap * 96, 4, 384), "head_dim 64"),
+                        (64, (H * tcap * 64, tcap * 64, 4, 240), "v_sq >= 4"),
+                        (64, (H * tcap * 64, tcap * 64, 4, 264), "v_sq % 16"),
+                        (64, (H * tcap * 64, tcap * 64, 8, 256), "v_sd == 4")):
+        with pytest.raises(RuntimeError, match=what):
+            iw._lib.call("iw_attention_decode_cache", q.data_ptr(), H * D, k.data_ptr(), H * tcap * D, tcap * D,
+                         D, v.data_ptr(), *vs, out.data_ptr(), H * D, B, H, D, 1, None, 1, 1, 1, 8, 1, 1, 16,
+                         stream())
+
+
+@pytest.mark.parametrize("layout", ["vt", "quads"])
+def test_attention_decode_cache_clamps_keys(iw, oracle, gpu, layout):
     """A device position past the cache reads max_keys keys, not beyond."""
     B, H, D, tcap = 1, 2, 64, 64
     q, k, v, qm, qs, f, am, as_ = gen.attn_case(77, B, H, 1, tcap, D)
     exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
     got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=1, pos_val=10_000,
-                        max_keys=tcap)
+                        max_keys=tcap, layout=layout)
     assert np.array_equal(got, exp)
 
 
-def test_attention_decode_cache_wrap_corner(iw, oracle, gpu):
+@pytest.mark.parametrize("layout", ["vt", "quads"])
+def test_attention_decode_cache_wrap_corner(iw, oracle, gpu, layout):
     B, H, D, Tk = 1, 1, 64, 40
     q = np.full((B, H, 1, D), 127, np.int8)
     k = np.full((B, H, Tk, D), 127, np.int8)
@@ -86,17 +123,18 @@ def test_attention_decode_cache_wrap_corner(iw, oracle, gpu):
     v = gen.i8(gen.rng(1), (B, H, D, Tk))
     exp = oracle.attention(q, k, v, None, 255, 0, 8, 200, 6)
     got = _decode_cache(iw, q, k, v, 255, 0, 8, 200, 6, tcap=448, k_length=1, pos_val=Tk - 1,
-                        max_keys=448)
+                        max_keys=448, layout=layout)
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("layout", ["vt", "quads"])
 @pytest.mark.parametrize("wrap_head", [0, 1])
 @pytest.mark.parametrize("B,H,Tk,tcap", [(1, 2, 700, 1024), (3, 4, 1500, 1500), (2, 2, 40, 448)])
-def test_attention_decode_cache_heads_share_a_block(iw, oracle, gpu, wrap_head, B, H, Tk, tcap):
+def test_attention_decode_cache_heads_share_a_block(iw, oracle, gpu, wrap_head, B, H, Tk, tcap, layout):
     """Cross-attention-sized caches run two heads per block as one stream: each
     head's row maximum, P, sums and wrap flag must stay its own. One head of
     every pair takes the int16 row-max wrap (P = 128), the other does not."""
-    print("case: heads share a block", wrap_head, B, H, Tk, tcap, flush=True)
+    print("case: heads share a block", wrap_head, B, H, Tk, tcap, layout, flush=True)
     D = 64
     q, k, v, qm, qs, f, am, as_ = gen.attn_case(11 * B + H + Tk, B, H, 1, Tk, D)
     for h in range(wrap_head, H, 2):
@@ -105,30 +143,33 @@ def test_attention_decode_cache_heads_share_a_block(iw, oracle, gpu, wrap_head, 
         k[:, h, 1::3] = -128
     qm, qs, f = 255, 0, 8
     exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
-    got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=Tk, pos_val=None, max_keys=Tk)
+    got = _decode_cache(iw, q, k, v, qm, qs, f, am, as_, tcap=tcap, k_length=Tk, pos_val=None, max_keys=Tk,
+                        layout=layout)
     assert np.array_equal(got, exp)
 
 
 @pytest.mark.parametrize("B,Tn,H,D,pos_val,tcap", [(1, 1, 2, 64, 0, 448), (5, 1, 2, 64, 7, 448),
                                                     (128, 1, 2, 64, 100, 448), (4, 3, 2, 64, 0, 448),
-                                                    (2, 3, 4, 32, 38, 40), (40, 3, 2, 64, 5, 448)])
-def test_linear8_qkv_cache(iw, oracle, gpu, B, Tn, H, D, pos_val, tcap):
-    print("case: qkv cache", B, Tn, H, D, pos_val, tcap, flush=True)
+                                                    (2, 3, 4, 32, 38, 40), (40, 3, 2, 64, 5, 448),
+                                                    (3, 3, 2, 64, 446, 448)])
+@pytest.mark.parametrize("layout", gen.V_LAYOUTS)
+def test_linear8_qkv_cache(iw, oracle, gpu, B, Tn, H, D, pos_val, tcap, layout):
+    print("case: qkv cache", B, Tn, H, D, pos_val, tcap, layout, flush=True)
     C = H * D
     M = B * Tn
     x, w, b, z, m, s = gen.realistic_linear_case(M + C + pos_val, M, C, 3 * C)
     exp = oracle.linear8(x, w, b, z, m, s)
     r = gen.rng(5)
-    tc16 = (tcap + 15) // 16 * 16
     kc0 = gen.i8(r, (B, H, tcap, D))
-    vc0 = gen.i8(r, (B, H, D, tc16))
+    shape, vs = gen.v_cache_layout(B, H, D, tcap, layout)
+    vc0 = gen.i8(r, shape)
     kc, vc = T(kc0), T(vc0)
     q = torch.empty((M, C), dtype=torch.int8, device="cuda")
     pos = torch.tensor([pos_val], dtype=torch.int32, device="cuda")
     xt, wt, bt, zt, mt, st = T(x), T(w), T(b), T(z), T(m), T(s)  # alive across the call
     iw._lib.call("iw_linear8_qkv_cache", xt.data_ptr(), wt.data_ptr(), bt.data_ptr(), zt.data_ptr(),
                  mt.data_ptr(), st.data_ptr(), M, C, True, True, q.data_ptr(), C,
-                 kc.data_ptr(), H * tcap * D, tcap * D, D, vc.data_ptr(), H * D * tc16, D * tc16, tc16,
+                 kc.data_ptr(), H * tcap * D, tcap * D, D, vc.data_ptr(), *vs,
                  C, D, Tn, tcap, pos.data_ptr(), stream())
     torch.cuda.synchronize()
     assert np.array_equal(host(q), exp[:, :C])
@@ -138,28 +179,31 @@ def test_linear8_qkv_cache(iw, oracle, gpu, B, Tn, H, D, pos_val, tcap):
         t = pos_val + i
         if t < tcap:
             kexp[:, :, t, :] = e[:, i, 1]
-            vexp[:, :, :, t] = e[:, i, 2]
+            gen.v_cache_put(vexp, layout, t, e[:, i, 2][..., None])
     assert np.array_equal(host(kc), kexp)
     assert np.array_equal(host(vc), vexp)
 
 
 @pytest.mark.parametrize("B,T,H,D,t_off", [(2, 1500, 4, 64, 0), (1, 37, 2, 64, 16), (3, 64, 3, 32, 0),
                                            (2, 100, 2, 64, 3), (1, 5, 2, 48, 0)])
-def test_transpose_heads(iw, gpu, B, T, H, D, t_off):
-    """V of a fused [B, T, 3C] projection into per-head transposed [B, H, D, Tcap]
-    rows at positions t_off .. t_off + T; every other byte is left as it was."""
-    print("case: transpose heads", B, T, H, D, t_off, flush=True)
+@pytest.mark.parametrize("layout", gen.V_LAYOUTS)
+def test_transpose_heads(iw, gpu, B, T, H, D, t_off, layout):
+    """V of a fused [B, T, 3C] projection into a per-head V cache (transposed
+    rows or key quads) at positions t_off .. t_off + T; every other byte is
+    left as it was."""
+    print("case: transpose heads", B, T, H, D, t_off, layout, flush=True)
     C = H * D
     r = gen.rng(T + t_off)
     qkv = gen.i8(r, (B, T, 3 * C))
     tcap = (t_off + T + 15) // 16 * 16 + 16
-    dst0 = np.full((B, H, D, tcap), 0x55, np.int8)
+    shape, vs = gen.v_cache_layout(B, H, D, tcap, layout)
+    dst0 = np.full(shape, 0x55, np.int8)
     src, dst = T_(qkv), T_(dst0)
-    iw._lib.call("iw_transpose_heads", src.data_ptr() + 2 * C, T * 3 * C, 3 * C, dst.data_ptr(), H * D * tcap,
-                 D * tcap, tcap, t_off, B, T, H, D, stream())
+    iw._lib.call("iw_transpose_heads", src.data_ptr() + 2 * C, T * 3 * C, 3 * C, dst.data_ptr(), *vs,
+                 t_off, B, T, H, D, stream())
     torch.cuda.synchronize()
     exp = dst0.copy()
-    exp[:, :, :, t_off:t_off + T] = qkv[:, :, 2 * C:].reshape(B, T, H, D).transpose(0, 2, 3, 1)
+    gen.v_cache_put(exp, layout, t_off, qkv[:, :, 2 * C:].reshape(B, T, H, D).transpose(0, 2, 3, 1))
     assert np.array_equal(host(dst), exp)
 
 

@@ -190,24 +190,26 @@ def test_frag_prefetch_hint_is_checked(iw, gpu):
                          of.data_ptr(), 4, 384, False, ptr, n, k, stream())
 
 
-@pytest.mark.parametrize("B,H,D,Tk,tcap,k_length", [(2, 3, 64, 17, 448, 1), (128, 20, 64, 1500, 1500, 1500),
-                                                    (3, 4, 96, 100, 448, 1), (1, 2, 128, 300, 448, 1)])
-def test_attention_decode_cache_frag(iw, oracle, gpu, B, H, D, Tk, tcap, k_length):
-    print("case: decode cache frag", B, H, D, Tk, tcap, k_length, flush=True)
+@pytest.mark.parametrize("B,H,D,Tk,tcap,k_length,layout", [
+    (2, 3, 64, 17, 448, 1, "vt"), (128, 20, 64, 1500, 1500, 1500, "vt"), (3, 4, 96, 100, 448, 1, "vt"),
+    (1, 2, 128, 300, 448, 1, "vt"), (2, 3, 64, 17, 448, 1, "quads"), (128, 20, 64, 301, 448, 1, "quads"),
+    (5, 20, 64, 448, 448, 1, "quads_pad")])
+def test_attention_decode_cache_frag(iw, oracle, gpu, B, H, D, Tk, tcap, k_length, layout):
+    print("case: decode cache frag", B, H, D, Tk, tcap, k_length, layout, flush=True)
     q, k, v, qm, qs, f, am, as_ = gen.attn_case(5 * B + Tk + D, B, H, 1, Tk, D)
     exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_).reshape(B, H * D)
-    tc16 = (tcap + 15) // 16 * 16
     kc = np.zeros((B, H, tcap, D), np.int8)
-    vc = np.zeros((B, H, D, tc16), np.int8)
+    shape, vs = gen.v_cache_layout(B, H, D, tcap, layout)
+    vc = np.zeros(shape, np.int8)
     kc[:, :, :Tk] = k
-    vc[..., :Tk] = v  # attn_case gives V transposed, [B, H, D, Tk]
+    gen.v_cache_put(vc, layout, 0, v)  # attn_case gives V transposed, [B, H, D, Tk]
     qt, kt, vt = T(q.reshape(B, H * D)), T(kc), T(vc)
     pos_val = None if k_length == Tk else Tk - k_length
     pos = None if pos_val is None else torch.tensor([pos_val], dtype=torch.int32, device="cuda")
     max_keys = tcap if pos is not None else k_length
     of = zeros_frag(iw, B, H * D)
     iw._lib.call("iw_attention_decode_cache_frag", qt.data_ptr(), H * D, kt.data_ptr(), H * tcap * D, tcap * D,
-                 D, vt.data_ptr(), H * D * tc16, D * tc16, tc16, of.data_ptr(), B, H, D, k_length,
+                 D, vt.data_ptr(), *vs, of.data_ptr(), B, H, D, k_length,
                  None if pos is None else pos.data_ptr(), max_keys, qm, qs, f, am, as_, 16, stream())
     torch.cuda.synchronize()
     assert np.array_equal(host(of), frag_image(exp))
@@ -215,15 +217,16 @@ def test_attention_decode_cache_frag(iw, oracle, gpu, B, H, D, Tk, tcap, k_lengt
 
 @pytest.mark.parametrize("B,H,D,pos_val,tcap", [(128, 20, 64, 100, 448), (5, 6, 64, 447, 448),
                                                 (3, 4, 96, 0, 448), (2, 2, 64, 40, 40)])
-def test_linear8_qkv_cache_frag(iw, oracle, gpu, B, H, D, pos_val, tcap):
-    print("case: qkv cache frag", B, H, D, pos_val, tcap, flush=True)
+@pytest.mark.parametrize("layout", gen.V_LAYOUTS)
+def test_linear8_qkv_cache_frag(iw, oracle, gpu, B, H, D, pos_val, tcap, layout):
+    print("case: qkv cache frag", B, H, D, pos_val, tcap, layout, flush=True)
     C = H * D
     x, w, b, z, m, s = gen.realistic_linear_case(B + C + pos_val, B, C, 3 * C)
     exp = oracle.linear8(x, w, b, z, m, s)
     r = gen.rng(9)
-    tc16 = (tcap + 15) // 16 * 16
     kc0 = gen.i8(r, (B, H, tcap, D))
-    vc0 = gen.i8(r, (B, H, D, tc16))
+    shape, vs = gen.v_cache_layout(B, H, D, tcap, layout)
+    vc0 = gen.i8(r, shape)
     kc, vc = T(kc0), T(vc0)
     q = torch.empty((B, C), dtype=torch.int8, device="cuda")
     pos = torch.tensor([pos_val], dtype=torch.int32, device="cuda")
@@ -231,14 +234,14 @@ def test_linear8_qkv_cache_frag(iw, oracle, gpu, B, H, D, pos_val, tcap):
     ts = [T(a) for a in (b, z, m, s)]
     iw._lib.call("iw_linear8_qkv_cache_frag", xf.data_ptr(), wf.data_ptr(), *[t.data_ptr() for t in ts], B, C,
                  True, True, q.data_ptr(), C, kc.data_ptr(), H * tcap * D, tcap * D, D, vc.data_ptr(),
-                 H * D * tc16, D * tc16, tc16, C, D, 1, tcap, pos.data_ptr(), stream())
+                 *vs, C, D, 1, tcap, pos.data_ptr(), stream())
     torch.cuda.synchronize()
     assert np.array_equal(host(q), exp[:, :C])
     kexp, vexp = kc0.copy(), vc0.copy()
     e = exp.reshape(B, 3, H, D)
     if pos_val < tcap:
         kexp[:, :, pos_val, :] = e[:, 1]
-        vexp[:, :, :, pos_val] = e[:, 2]
+        gen.v_cache_put(vexp, layout, pos_val, e[:, 2][..., None])
     assert np.array_equal(host(kc), kexp)
     assert np.array_equal(host(vc), vexp)
 
