@@ -849,6 +849,10 @@ __device__ __forceinline__ void lds_barrier() {
 #ifndef IW_DSS_NW
 #define IW_DSS_NW 4
 #endif
+// waves per (batch, head) of the register-resident self-attention kernel
+#ifndef IW_DSELF_NW
+#define IW_DSELF_NW 4
+#endif
 
 template <int MAXK, int NR, int CH, int NW = 4, bool VQ = false>
 __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
@@ -1068,6 +1072,216 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode self-attention over a V cache in key quads, at most 512 keys: every
+// load of K and V is issued at the start, into registers.
+//
+// A self-attention cache holds at most n_text_ctx (448) positions, so one
+// (batch, head) pair is at most 56 KB of K and V, which NW waves hold in
+// registers (per 16 NW-key chunk and wave: 16 keys of K and 4 quads of V,
+// 8 VGPRs). A block issues every load before it waits for any, so it lives
+// for about one memory latency plus its transfer, where a ring of chunks
+// waits chunk by chunk.
+//
+// Lanes, chunk c of wave w (keys c*16NW + 16w + 0..15):
+//   K lane l: key 4 (l/16) + l%4, bytes 16 p .. +15 with p = (l/4) % 4. The
+//     four lanes of a key are one orbit of rotation by 4 inside a 16-lane
+//     row, so two DPP adds complete its score in each of them.
+//   V lane l: quad 4 (l/16) (keys 4 (l/16) + 0..3), d = 4 (l%16) .. +3.
+// Every K lane holds every chunk's score of its key; lane p of the orbit
+// keeps chunks 4g + p, so the requantization, the shift-exp and the P sum run
+// once per key and chunk, NC/4 times per lane. The P of keys 4 (l/16) + 0..3
+// are then one DPP quad, packed into a word by quad broadcasts; a V lane
+// takes the word of its chunk from lane 16 (l/16) + 4 (c%4) (one bpermute).
+// Two block barriers: the row maximum, and the final sums of P and P.V. NC
+// (chunks) is a template argument, so that each case issues exactly its
+// loads; the kernel switches on the chunk count of the device-side key count.
+// ---------------------------------------------------------------------------
+
+template <int NW>
+struct SelfDecodeLds {
+  uint32_t part[NW * 64];  // per wave: P.V sums of d = 0 .. 63
+  int32_t mx[NW];
+  uint32_t sum[NW];
+};
+
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_mov(int32_t x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, true);
+}
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+template <int J>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t x) {
+  return (uint32_t)dpp_mov<J | (J << 2) | (J << 4) | (J << 6)>((int32_t)x);
+}
+
+template <int NW>
+__device__ __forceinline__ void self_decode_store(const AttnArgs &a, int64_t b, int h, uint32_t v, uint32_t total,
+                                                  int d) {
+  const int32_t inv = fisr((int32_t)total, a.rsqrt_off);
+  int32_t y = rshift((int32_t)(v * (uint32_t)inv), a.rsqrt_off);
+  y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+  y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
+  a.out[decode_out_index(a, b, h * 64 + d)] = (int8_t)clampi(y, -127, 127);
+}
+
+template <int NW, int NC>
+__device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, int h, int Tk,
+                                                 SelfDecodeLds<NW> &sm) {
+  constexpr int CK = 16 * NW;       // keys per chunk
+  constexpr int NG = (NC + 3) / 4;  // scores per lane after the regrouping
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int piece = (lane >> 2) & 3;
+  const int kl = wave * 16 + ((lane >> 4) << 2) + (lane & 3);  // key of this K lane in a chunk
+  const int ql = wave * 4 + (lane >> 4);                       // quad of this V lane in a chunk
+  const int8_t *kb = a.k + b * a.k_sb + (int64_t)h * a.k_sh;
+  const int8_t *vb = a.vt + b * a.v_sb + (int64_t)h * a.v_sh;
+  // 32-bit offsets inside the head (the launcher checks the cache extent)
+  const uint32_t k_st = (uint32_t)a.k_st, v_sq = (uint32_t)a.v_sq;
+  const uint32_t koff = (uint32_t)kl * k_st + piece * 16, voff = (uint32_t)ql * v_sq + (lane & 15) * 16;
+
+  const v4i qv = *reinterpret_cast<const v4i *>(a.q + b * a.q_sb + (int64_t)h * 64 + piece * 16);
+  v4i kx[NC], vx[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    // the last chunk reads the last valid key / quad in place of those past Tk
+    const uint32_t off = c < NC - 1 ? (uint32_t)(c * CK) * k_st + koff
+                                    : (uint32_t)min(c * CK + kl, Tk - 1) * k_st + piece * 16;
+    kx[c] = *reinterpret_cast<const v4i *>(kb + off);
+  }
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const uint32_t off = c < NC - 1 ? (uint32_t)(c * 4 * NW) * v_sq + voff
+                                    : (uint32_t)min(c * 4 * NW + ql, (Tk - 1) >> 2) * v_sq + (lane & 15) * 16;
+    vx[c] = *reinterpret_cast<const v4i *>(vb + off);
+  }
+  // every load is issued before the first wait (the scheduler would
+  // otherwise defer the V loads to reuse registers)
+  __builtin_amdgcn_sched_barrier(0);
+
+  int32_t dot[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    int32_t d = __builtin_amdgcn_sdot4(qv[0], kx[c][0], 0, false);
+    d = __builtin_amdgcn_sdot4(qv[1], kx[c][1], d, false);
+    d = __builtin_amdgcn_sdot4(qv[2], kx[c][2], d, false);
+    d = __builtin_amdgcn_sdot4(qv[3], kx[c][3], d, false);
+    d += dpp_mov<kDppRowRor8>(d);
+    dot[c] = d + dpp_mov<kDppRowRor4>(d);
+  }
+  // lane p of a key's orbit keeps chunks 4 g + p: scores requantized to
+  // int16 (qk_requant16) and their maximum over the valid keys
+  int32_t sc[NG];
+  int32_t mx = -32768;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    int32_t d = dot[4 * g];
+#pragma unroll
+    for (int r = 1; r < 4; ++r)
+      if (4 * g + r < NC && piece == r) d = dot[4 * g + r];
+    sc[g] = qk_requant16(d, a.qk_m, a.qk_s);
+    const int c = 4 * g + piece;
+    if (c < NC && c * CK + kl < Tk) mx = max(mx, sc[g]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  if (lane == 0) sm.mx[wave] = mx;
+  lds_barrier();
+  int32_t rowmax = sm.mx[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) rowmax = max(rowmax, sm.mx[w]);
+
+  // P = shift_exp(score - (rowmax + 1)) in int16 arithmetic, 0 past Tk; the
+  // word of keys 4 (l/16) + 0..3 of chunk 4 g + (l/4) % 4 in every lane
+  const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
+  uint32_t psum = 0, hi = 0;
+  uint32_t pword[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const int c = 4 * g + piece;
+    uint32_t p = 0;
+    if (c < NC && c * CK + kl < Tk)
+      p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)sc[g] - rmp1), a.frac_bits);
+    psum += p;
+    hi |= p;
+    pword[g] = quad_bcast<0>(p) | (quad_bcast<1>(p) << 8) | (quad_bcast<2>(p) << 16) | (quad_bcast<3>(p) << 24);
+  }
+  // P = 128 only after an int16 row-max wrap: then the top bit is split off
+  const bool whi = __any(hi & 0x80u);
+  uint32_t acc[4] = {0, 0, 0, 0};
+  int32_t hs[4] = {0, 0, 0, 0};
+  const int src = (lane & 48) * 4;  // bpermute byte address of lane 16 (l/16)
+  if (!whi) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(src + (c & 3) * 16, (int)pword[c >> 2]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = (uint32_t)__builtin_amdgcn_sdot4((int)pw, vx[c][j], (int)acc[j], false);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const uint32_t pw = (uint32_t)__builtin_amdgcn_ds_bpermute(src + (c & 3) * 16, (int)pword[c >> 2]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw & 0x7f7f7f7fu), vx[c][j], (int)acc[j], false);
+        hs[j] = __builtin_amdgcn_sdot4((int)((pw >> 7) & 0x01010101u), vx[c][j], hs[j], false);
+      }
+    }
+  }
+  // lanes l, l ^ 16, l ^ 32, l ^ 48 hold other quads of the same d
+  uint4 v;
+  uint32_t *vw = &v.x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t t = acc[j] + ((uint32_t)hs[j] << 7);
+    t += (uint32_t)__shfl_xor((int)t, 16);
+    vw[j] = t + (uint32_t)__shfl_xor((int)t, 32);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) psum += (uint32_t)__shfl_xor((int)psum, off);
+  if (lane < 16) *reinterpret_cast<uint4 *>(&sm.part[wave * 64 + 4 * lane]) = v;
+  if (lane == 0) sm.sum[wave] = psum;
+  lds_barrier();
+  if (tid < 64) {
+    uint32_t total = 0, pv = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      total += sm.sum[w];
+      pv += sm.part[w * 64 + tid];
+    }
+    self_decode_store<NW>(a, b, h, pv, total, tid);
+  }
+}
+
+template <int NW, int NC>
+__device__ __forceinline__ void self_decode_dispatch(int nc, const AttnArgs &a, int64_t b, int h, int Tk,
+                                                     SelfDecodeLds<NW> &sm) {
+  if constexpr (NC == 0) {
+    // no keys: every sum is 0
+    if (threadIdx.x < 64) self_decode_store<NW>(a, b, h, 0u, 0u, threadIdx.x);
+  } else {
+    if (nc == NC)
+      self_decode_body<NW, NC>(a, b, h, Tk, sm);
+    else
+      self_decode_dispatch<NW, NC - 1>(nc, a, b, h, Tk, sm);
+  }
+}
+
+// at most 16 NW NCMAX keys
+template <int NW, int NCMAX>
+__global__ __launch_bounds__(64 * NW) void attn_decode_self_kernel(AttnArgs a, const int32_t *pos) {
+  __shared__ __attribute__((aligned(16))) SelfDecodeLds<NW> sm;
+  const int64_t bh = blockIdx.x;
+  const int h = (int)(bh % a.H);
+  const int64_t b = bh / a.H;
+  const int Tk = min(a.Tk + (pos ? *pos : 0), a.max_tk);
+  const int nc = (Tk + 16 * NW - 1) / (16 * NW);
+  self_decode_dispatch<NW, NCMAX>(nc, a, b, h, Tk, sm);
+}
+
 }  // namespace
 
 int launch_qk_requant_rowmax(const int8_t *q, const int8_t *k, const uint8_t *mask, int16_t *qk,
@@ -1154,6 +1368,21 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
   else                                                                                                         \
     hipLaunchKernelGGL((attn_decode_stream_kernel<DC_MAX_TK, IW_DS_NR, IW_DS_CH, 4, VQ_>), grid, dim3(256), 0, \
                        s, a, pos);
+    // (32-bit offsets inside a head's K rows and V quads)
+    const bool off32 = (int64_t)a.max_tk * a.k_st < (1ll << 31) && (int64_t)(a.max_tk + 3) / 4 * a.v_sq < (1ll << 31);
+    if (vq && a.max_tk <= 16 * IW_DSELF_NW * 8 && off32) {
+      // self-attention caches: every load in flight at once
+      const int ncmax = (a.max_tk + 16 * IW_DSELF_NW - 1) / (16 * IW_DSELF_NW);
+      if (ncmax <= 2)
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 2>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+      else if (ncmax <= 4)
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 4>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+      else if (ncmax <= 7)
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 7>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+      else
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 8>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+      return check_launch("attn_decode_self_kernel");
+    }
     if (vq) {
       IW_DS(true)
     } else {
