@@ -194,11 +194,11 @@ def test_layernorm32(iw, oracle, gpu, hidden, rows, spread):
 
 
 @pytest.mark.parametrize("hidden", [384, 1280])
-@pytest.mark.parametrize("rows", [6, 2100])
+@pytest.mark.parametrize("rows", [6, 200, 2100])
 def test_layernorm32_full_int16_range(iw, oracle, gpu, hidden, rows):
     """Rows whose deviations from the mean exceed 46340, where d^2 wraps in int32
     (the kernels' per-element form), next to ordinary rows in the same launch:
-    one row-per-block launch (<= 2048 rows) and one persistent-wave launch."""
+    row-per-block launches (<= 2048 rows) and one persistent-wave launch."""
     _print_case("layernorm32 full int16 range", hidden, rows)
     x, g, b, lm, ls, om, os_ = gen.ln_case(hidden + rows + 1, rows, hidden, 3000)
     r = gen.rng(rows)
