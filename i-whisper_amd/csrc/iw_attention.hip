@@ -863,6 +863,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   constexpr int WB = 1024 * DPC;      // bytes per wave per slot
   constexpr int LPR = CH / 16;        // lanes per V^T row piece set
   constexpr int RPD = 64 / LPR;       // V^T rows per copy
+  static_assert(LPR == 4 || LPR == 8 || LPR == 16, "a V^T row's lanes are 4, 8 or 16 of one 16-lane row");
   constexpr int NACC = VQ ? 4 : DPC;  // P.V sums per lane
   static_assert(!VQ || NW * 64 * 4 <= MAXK * 2, "the wave sums of P.V fit in the score array");
   __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
@@ -937,8 +938,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
 
   // row maximum, P and its sum once every score is in sS
   auto form_p = [&]() {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+    mx = wave_max_dpp(mx);
     if (lane == 0) sRed[wave] = mx;
     lds_barrier();
     int32_t rowmax = sRed[0];
@@ -954,8 +954,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
       psum += p;
       hi |= p;
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) psum += (uint32_t)__shfl_xor((int)psum, off);
+    psum = wave_sum_dpp(psum);
     if (lane == 0) sSum[wave] = psum;
     if (hi & 0x80u) atomicOr(&sHi, 1u);
     lds_barrier();
@@ -989,8 +988,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
         acc = __builtin_amdgcn_sdot4(qv[1], x[u][1], acc, false);
         acc = __builtin_amdgcn_sdot4(qv[2], x[u][2], acc, false);
         acc = __builtin_amdgcn_sdot4(qv[3], x[u][3], acc, false);
-        acc += __shfl_xor(acc, 1);
-        acc += __shfl_xor(acc, 2);
+        acc = quad_sum_dpp(acc);  // the key's four 16-byte pieces
         const int j = i * CH + kkey + 16 * u;
         if (j < Tk) {
           const int32_t h16 = qk_requant16(acc, a.qk_m, a.qk_s);
@@ -1064,10 +1062,12 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   } else {
 #pragma unroll
     for (int u = 0; u < DPC; ++u) {
-      uint32_t v = accd[u] + ((uint32_t)hs[u] << 7);
-#pragma unroll
-      for (int o = 1; o < LPR; o <<= 1) v += (uint32_t)__shfl_xor((int)v, o);
-      if (vp == 0) store(v, vrow + u * RPD);
+      // the row's LPR lanes l .. l + LPR - 1 (l % LPR == 0): quad sums, then
+      // row_shl:4 / :8 (lane i reads lane i + n of its 16-lane row) into l
+      int32_t v = quad_sum_dpp((int32_t)(accd[u] + ((uint32_t)hs[u] << 7)));
+      if (LPR >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, true);
+      if (LPR >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0xf, true);
+      if (vp == 0) store((uint32_t)v, vrow + u * RPD);
     }
   }
 }
@@ -1100,7 +1100,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
 
 template <int NW>
 struct SelfDecodeLds {
-  uint32_t part[NW * 64];  // per wave: P.V sums of d = 0 .. 63
+  uint4 part[NW * 64];  // per wave and lane: P.V sums of d = 4 (l % 16) .. +3
   int32_t mx[NW];
   uint32_t sum[NW];
 };
@@ -1185,8 +1185,7 @@ __device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, i
     const int c = 4 * g + piece;
     if (c < NC && c * CK + kl < Tk) mx = max(mx, sc[g]);
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+  mx = wave_max_dpp(mx);
   if (lane == 0) sm.mx[wave] = mx;
   lds_barrier();
   int32_t rowmax = sm.mx[0];
@@ -1231,26 +1230,21 @@ __device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, i
       }
     }
   }
-  // lanes l, l ^ 16, l ^ 32, l ^ 48 hold other quads of the same d
-  uint4 v;
-  uint32_t *vw = &v.x;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t t = acc[j] + ((uint32_t)hs[j] << 7);
-    t += (uint32_t)__shfl_xor((int)t, 16);
-    vw[j] = t + (uint32_t)__shfl_xor((int)t, 32);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) psum += (uint32_t)__shfl_xor((int)psum, off);
-  if (lane < 16) *reinterpret_cast<uint4 *>(&sm.part[wave * 64 + 4 * lane]) = v;
+  // every lane's sums go to LDS; d = 4 (l % 16) + j is summed over the
+  // lanes l % 16 + 16 r of every wave
+  sm.part[wave * 64 + lane] = make_uint4(acc[0] + ((uint32_t)hs[0] << 7), acc[1] + ((uint32_t)hs[1] << 7),
+                                         acc[2] + ((uint32_t)hs[2] << 7), acc[3] + ((uint32_t)hs[3] << 7));
+  psum = wave_sum_dpp(psum);
   if (lane == 0) sm.sum[wave] = psum;
   lds_barrier();
   if (tid < 64) {
+    const uint32_t *pw = reinterpret_cast<const uint32_t *>(sm.part) + (tid >> 2) * 4 + (tid & 3);
     uint32_t total = 0, pv = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       total += sm.sum[w];
-      pv += sm.part[w * 64 + tid];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pv += pw[(w * 64 + 16 * r) * 4];
     }
     self_decode_store<NW>(a, b, h, pv, total, tid);
   }

@@ -111,6 +111,37 @@ __device__ inline uint32_t shift_exp_one(int32_t x_sub16, int32_t f) {
   return (uint32_t)(uint8_t)o;
 }
 
+// Sum over the four lanes of a DPP quad (xor-1 and xor-2 quad permutes), in
+// every lane of it.
+__device__ __forceinline__ int32_t quad_sum_dpp(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);  // quad [1,0,3,2]
+  return v + __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);  // quad [2,3,0,1]
+}
+
+// Wave-wide sum / max with DPP moves (no LDS round trips): xor-1 and xor-2
+// quad permutes, then the half-row and row mirrors give every lane its
+// 16-lane row's total; the four rows are added from lanes 0, 16, 32, 48.
+__device__ __forceinline__ uint32_t row16_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true);   // quad [1,0,3,2]
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true);   // quad [2,3,0,1]
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, true);  // row_half_mirror
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, true);  // row_mirror
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_dpp(uint32_t v) {
+  v = row16_sum(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+}
+__device__ __forceinline__ int32_t wave_max_dpp(int32_t v) {
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0xB1, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x4E, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x141, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT32_MIN, v, 0x140, 0xf, 0xf, false));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 }  // namespace iw
 
 // ---------------------------------------------------------------------------
