@@ -16,6 +16,8 @@
 // Integer sums are exact modulo 2^32 in any order, so the zero-point term
 // wz[n] * rowsum(A[m]) is formed from per-row sums taken with v_dot4 while
 // the A tile passes through registers, and added in the epilogue.
+#include <algorithm>
+
 #include "iw_gemm_dev.hpp"
 
 namespace iw {
@@ -220,6 +222,25 @@ int gemm_dense(const GemmArgs &g, hipStream_t s) {
   const bool afast = g.K % 16 == 0 && g.lda % 16 == 0 && aligned16(g.a);
   const bool bfast = g.K % 16 == 0 && g.ldb % 16 == 0 && aligned16(g.b);
   if (gemm_skinny_eligible(g)) return gemm_skinny(g, nullptr, s);
+  if (g.M > kSkinnyMaxRows && g.M <= kSkinnyChunkMaxRows) {
+    // a few hundred rows (the decoder's prompt step): the decode kernel over
+    // chunks of 128 rows, whose launches cost less than one launch of the
+    // tile kernel at this size
+    GemmArgs c = g;
+    c.M = kSkinnyMaxRows;
+    if (gemm_skinny_eligible(c)) {
+      const int64_t esz = g.epi == EPI_L32 ? 4 : (g.epi == EPI_L32RES ? 2 : 1);  // output bytes
+      for (int64_t r0 = 0; r0 < g.M; r0 += kSkinnyMaxRows) {
+        c.M = std::min<int64_t>(kSkinnyMaxRows, g.M - r0);
+        c.a = g.a + r0 * g.lda;
+        c.out = static_cast<int8_t *>(g.out) + r0 * g.ldc * esz;
+        if (g.res) c.res = g.res + r0 * g.ldres;
+        const int rc = gemm_skinny(c, nullptr, s);
+        if (rc) return rc;
+      }
+      return 0;
+    }
+  }
   if (g.M >= kBigGemmMinRows && gemm_dtl_eligible(g)) return gemm_dtl(g, s);
   if (afast && bfast && g.M >= kBigGemmMinRows) return gemm_big(g, false, s);
   switch (g.epi) {

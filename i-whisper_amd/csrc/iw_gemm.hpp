@@ -100,8 +100,13 @@ struct SkinnyScatter {
   const int32_t *pos = nullptr;
 };
 
-// Rows up to which the decode kernel (iw_gemm_skinny.hip) is used.
+// Rows up to which the decode kernel (iw_gemm_skinny.hip) is used, and up to
+// which it runs over 128-row chunks.
 constexpr int64_t kSkinnyMaxRows = 128;
+#ifndef IW_SKINNY_CHUNK_ROWS
+#define IW_SKINNY_CHUNK_ROWS 512
+#endif
+constexpr int64_t kSkinnyChunkMaxRows = IW_SKINNY_CHUNK_ROWS;
 bool gemm_skinny_eligible(const GemmArgs &g);
 int gemm_skinny(const GemmArgs &g, const SkinnyScatter *scatter, hipStream_t s);
 
