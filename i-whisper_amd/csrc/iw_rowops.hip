@@ -744,8 +744,9 @@ __global__ __launch_bounds__(256) void greedy_filtered_kernel(const int8_t *__re
   }
 }
 
-// The sum of e[x + 128] over the int8 values x of one row (256 threads, the
+// The sum of e[x + 128] over the int8 values x of one row (NT threads, the
 // row read in 16-byte pieces from its first 16-byte boundary), in float32.
+template <int NT = 256>
 __device__ __forceinline__ float row_table_sum(const int8_t *xr, int n, const float *e) {
   const int tid = threadIdx.x;
   const int head = min((int)((16 - (reinterpret_cast<uintptr_t>(xr) & 15)) & 15), n);
@@ -754,7 +755,7 @@ __device__ __forceinline__ float row_table_sum(const int8_t *xr, int n, const fl
   float s = 0.f;
   if (tid < head) s += e[xr[tid] + 128];
   const uint4 *xa = reinterpret_cast<const uint4 *>(xr + head);
-  for (int c = tid; c < pieces; c += 256) {
+  for (int c = tid; c < pieces; c += NT) {
     const uint4 w = xa[c];
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -764,6 +765,9 @@ __device__ __forceinline__ float row_table_sum(const int8_t *xr, int n, const fl
   return s;
 }
 
+// Block sum of NT threads' values: wave sums, then the waves' sums added in
+// adjacent pairs ((w0 + w1) + (w2 + w3), ...).
+template <int NT = 256>
 __device__ __forceinline__ float block_sum_f32(float v, float *sh) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -771,7 +775,14 @@ __device__ __forceinline__ float block_sum_f32(float v, float *sh) {
   __syncthreads();
   if ((tid & 63) == 0) sh[tid >> 6] = v;
   __syncthreads();
-  return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  float t[NT / 64];
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) t[w] = sh[w];
+#pragma unroll
+  for (int n = NT / 128; n >= 1; n >>= 1)
+#pragma unroll
+    for (int i = 0; i < n; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+  return t[0];
 }
 
 // One step of GreedyDecoder.update (decoding.py:280-296) at temperature 0,
@@ -808,10 +819,15 @@ struct GreedyUpdate {
   uint32_t *arrive = nullptr;
 };
 
-__global__ __launch_bounds__(256) void greedy_update_kernel(GreedyUpdate p) {
+// 1024 threads per row: the row's 51865 table lookups (Whisper) spread over
+// four waves per SIMD rather than one
+constexpr int GU_NT = 1024;
+
+__global__ __launch_bounds__(GU_NT) void greedy_update_kernel(GreedyUpdate p) {
+  constexpr int NW = GU_NT / 64;
   __shared__ int32_t s_st;
-  __shared__ uint32_t s_k[4];
-  __shared__ float s_f[4];
+  __shared__ uint32_t s_k[NW];
+  __shared__ float s_f[NW];
   __shared__ float s_e[256];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = blockIdx.x;
@@ -820,7 +836,7 @@ __global__ __launch_bounds__(256) void greedy_update_kernel(GreedyUpdate p) {
   uint32_t key = 0;
   if (p.amax) {
     const uint16_t *ar = p.amax + row * p.tiles;
-    for (int64_t t = tid; t < p.tiles; t += 256) {
+    for (int64_t t = tid; t < p.tiles; t += GU_NT) {
       const uint32_t q = ar[t];
       if (q) {
         const uint32_t i = (uint32_t)t * 32u + (31u - (q & 31u));
@@ -829,21 +845,23 @@ __global__ __launch_bounds__(256) void greedy_update_kernel(GreedyUpdate p) {
     }
   } else {
     const int8_t *xr = p.logits + row * p.ld;
-    for (int i = tid; i < p.cols; i += 256)
+    for (int i = tid; i < p.cols; i += GU_NT)
       key = max(key, ((uint32_t)(xr[i] + 128) << 23) | (uint32_t)(0x7FFFFF - i));
   }
-  key = wave_max_u32(key);
+  key = (uint32_t)wave_max_dpp((int32_t)key);  // keys < 2^31
   if (lane == 0) s_k[wave] = key;
   __syncthreads();  // s_st, s_k
-  key = max(max(s_k[0], s_k[1]), max(s_k[2], s_k[3]));
+  key = s_k[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) key = max(key, s_k[w]);
   const int st = s_st;
   const int32_t vmax = (int32_t)(key >> 23) - 128;
   const int64_t idx = (int64_t)(0x7FFFFF - (key & 0x7FFFFF));
   float lp = 0.f;
   if (p.sum_logprobs) {
-    s_e[tid] = expf((float)(tid - 128 - vmax) * p.scale);
+    if (tid < 256) s_e[tid] = expf((float)(tid - 128 - vmax) * p.scale);
     __syncthreads();
-    lp = -logf(block_sum_f32(row_table_sum(p.logits + row * p.ld, p.cols, s_e), s_f));
+    lp = -logf(block_sum_f32<GU_NT>(row_table_sum<GU_NT>(p.logits + row * p.ld, p.cols, s_e), s_f));
   }
   if (tid == 0) {
     const int64_t prev = st >= 1 ? (st - 1 < p.hist_cols ? p.history[row * p.hist_ld + st - 1] : -1)
@@ -1210,7 +1228,7 @@ int launch_greedy_update(const uint16_t *amax, int64_t tiles, const int8_t *logi
   p.scale = scale;
   p.eot_count = eot_count;
   p.arrive = arrive;
-  hipLaunchKernelGGL(greedy_update_kernel, dim3((unsigned)rows), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(greedy_update_kernel, dim3((unsigned)rows), dim3(GU_NT), 0, s, p);
   return check_launch("greedy_update_kernel");
 }
 
