@@ -15,9 +15,10 @@
 //
 // Block = one 32 x 32 output tile (m-subtile x column tile); its K steps are
 // split over NW waves of SPW k32 steps each (NW = Kp / (32 SPW)).
-// The partial tiles meet in LDS, and all threads run the epilogue. Blocks of
-// one column tile share blockIdx % 8, i.e. one XCD, so the tile's weights
-// come from HBM once and from that XCD's L2 for the other m-subtiles.
+// The waves' partial tiles are added into one tile in LDS (ds_add), and all
+// threads run the epilogue. Blocks of one column tile share blockIdx % 8,
+// i.e. one XCD, so the tile's weights come from HBM once and from that XCD's
+// L2 for the other m-subtiles.
 #include "iw_gemm_dev.hpp"
 
 namespace iw {
@@ -50,14 +51,17 @@ __device__ __forceinline__ void classifier_argmax_store(const GemmArgs &g, const
 template <int EPI, bool GELU, bool SCATTER, bool OUT_FRAG, int SPW, int MAXW, int MINW, bool ARGMAX = false>
 __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, SkinnyScatter sc, int ms, int tiles,
                                                               int kp) {
-  constexpr int PLD = 33;  // LDS row stride of the partial tiles (words)
-  __shared__ int32_t sPart[MAXW * 32 * PLD];
-  __shared__ int32_t sXs[MAXW][32];
+  // the waves' partial tiles are added into one tile in LDS (ds_add); row
+  // stride 40 words puts the two 32-lane halves of each add (rows 4 apart)
+  // on disjoint halves of the 64 banks
+  constexpr int PLD = 40;
+  __shared__ int32_t sTile[32 * PLD];
+  __shared__ int32_t sXs[32];
   __shared__ uint8_t sLut[16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nt = blockDim.x, nw = nt >> 6;
+  const int nt = blockDim.x;
   const int bid = blockIdx.x;
   const int tile = (bid & 7) + 8 * (bid / (8 * ms));
   const int msub = (bid >> 3) % ms;
@@ -87,6 +91,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
   }
   int pos = 0;
   if (SCATTER) pos = *sc.pos;
+  for (int i = tid; i < 32 * PLD; i += nt) sTile[i] = 0;
+  if (tid < 32) sXs[tid] = 0;
 
   // then every operand load of this wave: SPW fragments of A and of B
   const int64_t kofs = (int64_t)wave * SPW * 1024 + lane * 16;
@@ -112,6 +118,12 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  // the zeroed tile is seen by every wave before any adds into it (an LDS-only
+  // barrier: the operand loads stay in flight)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
   // two accumulator chains so that consecutive MFMAs do not wait on each
   // other; row sums of A for the zero-point term from the same registers
   v16i acc[2];
@@ -124,16 +136,16 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
     xs = sum16v(fa[t], xs);
   }
 
-  // partial tiles [wave][row][PLD]. 32x32 MFMA layout: lane l holds column
-  // l % 32, register r row (r / 4) * 8 + (l / 32) * 4 + r % 4.
-  int32_t *part = sPart + wave * 32 * PLD;
+  // this wave's partial tile added into sTile[row][PLD] (sums modulo 2^32,
+  // in any order). 32x32 MFMA layout: lane l holds column l % 32, register r
+  // row (r / 4) * 8 + (l / 32) * 4 + r % 4.
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-    part[row * PLD + (lane & 31)] = (int32_t)((uint32_t)acc[0][r] + (uint32_t)acc[1][r]);
+    atomicAdd(&sTile[row * PLD + (lane & 31)], (int32_t)((uint32_t)acc[0][r] + (uint32_t)acc[1][r]));
   }
   xs += __shfl_xor(xs, 32);
-  if (lane < 32) sXs[wave][lane] = xs;
+  if (lane < 32) atomicAdd(&sXs[lane], xs);
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
   __syncthreads();
 
@@ -146,9 +158,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
       const int r = mr0 + mstep * j;
       const int m = m0 + r;
       if (r < 32) {  // uniform over each 32-thread group
-        uint32_t a = 0;
-        for (int w = 0; w < nw; ++w) a += (uint32_t)sPart[(w * 32 + r) * PLD + cl];
-        classifier_argmax_store(g, c, m, n, tile, n < N && m < M, a);
+        classifier_argmax_store(g, c, m, n, tile, n < N && m < M, (uint32_t)sTile[r * PLD + cl]);
       }
     }
     return;
@@ -164,14 +174,8 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
     const int r = mr0 + mstep * j;
     const int m = m0 + r;
     if (r < 32 && m < M) {
-      uint32_t a = 0;
-      int32_t xsum = 0;
-      for (int w = 0; w < nw; ++w) {
-        a += (uint32_t)sPart[(w * 32 + r) * PLD + cl];
-        xsum += sXs[w][r];
-      }
       skinny_store<EPI, GELU, SCATTER, OUT_FRAG>(g, sc, c, sLut, pos, m, n,
-                                                 corrected_k32k((int32_t)a, zp ? xsum : 0, c),
+                                                 corrected_k32k(sTile[r * PLD + cl], zp ? sXs[r] : 0, c),
                                                  EPI == EPI_L32RES ? resv[j] : 0);
     }
   }
