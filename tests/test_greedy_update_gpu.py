@@ -45,7 +45,9 @@ def test_classifier_argmax_frag(iw, oracle, gpu, M, K, N):
     for mult, shift in ((int(r.integers(2**28, 2**32)), 12), (0x80000000, 40), (777, 0)):
         want = oracle.classifier(x[None], w, mult, shift)[0]
         out = torch.empty((M, N), dtype=torch.int8, device="cuda")
-        rm = torch.zeros((M, tiles), dtype=torch.int16, device="cuda")
+        # the tile maxima with a guard region after them, which must stay untouched
+        guarded = torch.full((M * tiles + 64,), 0x5A5A, dtype=torch.int16, device="cuda")
+        rm = guarded[:M * tiles].view(M, tiles)
         iw._lib.call("iw_classifier_argmax_frag", xf.data_ptr(), wf.data_ptr(), mult, shift, out.data_ptr(),
                      rm.data_ptr(), M, K, N, stream())
         rm2 = torch.zeros((M, tiles), dtype=torch.int16, device="cuda")
@@ -55,6 +57,7 @@ def test_classifier_argmax_frag(iw, oracle, gpu, M, K, N):
         assert np.array_equal(host(out), want)
         assert np.array_equal(host(rm).view(np.uint16), tile_maxima(want))
         assert torch.equal(rm, rm2)
+        assert bool((guarded[M * tiles:] == 0x5A5A).all())
 
 
 def _planted_logits(rng, B, V, eot, step):
