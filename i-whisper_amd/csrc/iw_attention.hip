@@ -789,6 +789,12 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 // bytes of d = 4 (l % 16) .. +3 of one quad, and the lane's four sdot4 take
 // the same P word. Each wave sums its own quads, so the d sums of the NW
 // waves meet in LDS at the end.
+//
+// NQ > 1 (V^T): the a.Tq <= NQ query positions of a (batch, head) share the
+// stream (the decoder's prompt over the cross-attention cache): each chunk in
+// LDS is scored against, then weighted by, every query's P; query i at
+// q + b*q_sb + i*q_st, its output at out + b*o_sb + i*o_st. The queries are
+// loaded into registers behind the first chunks' copies.
 // ---------------------------------------------------------------------------
 
 template <int N>
@@ -854,7 +860,7 @@ __device__ __forceinline__ void lds_barrier() {
 #define IW_DSELF_NW 4
 #endif
 
-template <int MAXK, int NR, int CH, int NW = 4, bool VQ = false>
+template <int MAXK, int NR, int CH, int NW = 4, bool VQ = false, int NQ = 1>
 __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
   constexpr int D = 64;
   constexpr int DPC = CH / (16 * NW);  // copies per wave per chunk
@@ -866,11 +872,12 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   static_assert(LPR == 4 || LPR == 8 || LPR == 16, "a V^T row's lanes are 4, 8 or 16 of one 16-lane row");
   constexpr int NACC = VQ ? 4 : DPC;  // P.V sums per lane
   static_assert(!VQ || NW * 64 * 4 <= MAXK * 2, "the wave sums of P.V fit in the score array");
+  static_assert(NQ == 1 || !VQ, "several queries stream V transposed");
   __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
-  __shared__ __attribute__((aligned(16))) int16_t sS[MAXK];  // requantized scores
-  __shared__ __attribute__((aligned(16))) uint8_t sP[MAXK];
-  __shared__ int32_t sRed[NW];
-  __shared__ uint32_t sSum[NW];
+  __shared__ __attribute__((aligned(16))) int16_t sS[NQ * MAXK];  // requantized scores
+  __shared__ __attribute__((aligned(16))) uint8_t sP[NQ * MAXK];
+  __shared__ int32_t sRed[NQ][NW];
+  __shared__ uint32_t sSum[NQ][NW];
   __shared__ uint32_t sHi;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -915,53 +922,78 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
     }
   };
 
-  // q: lane l needs bytes 16 (l % 4) of the head's 64. It is copied first,
-  // into the last ring slot (free until chunk NR - 1), so the chunk waits
-  // cover it. (Counted as DPC copies: the waits below are in whole chunks.)
+  // q: lane l needs bytes 16 (l % 4) of the head's 64. One query is copied
+  // first, into the last ring slot (free until chunk NR - 1), so the chunk
+  // waits cover it (counted as DPC copies: the waits below are in whole
+  // chunks); several are loaded into registers after the first chunks.
+  if constexpr (NQ == 1) {
 #pragma unroll
-  for (int u = 0; u < DPC; ++u)
-    dma16_lds(a.q + b * a.q_sb + (int64_t)h * D + cq * 16, ring + (NR - 1) * SLOT + u * 1024);
+    for (int u = 0; u < DPC; ++u)
+      dma16_lds(a.q + b * a.q_sb + (int64_t)h * D + cq * 16, ring + (NR - 1) * SLOT + u * 1024);
+  }
 #pragma unroll
   for (int i = 0; i < NR - 1; ++i)
     if (i < T) issue(i);
+  v4i qv[NQ];
+  if constexpr (NQ > 1) {
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi)
+      qv[qi] = *reinterpret_cast<const v4i *>(a.q + b * a.q_sb + (int64_t)min(qi, a.Tq - 1) * a.q_st +
+                                              (int64_t)h * D + cq * 16);
+  } else {
+    qv[0] = v4i{0, 0, 0, 0};
+  }
 
-  int32_t mx = -32768;
-  uint32_t accd[NACC];
+  int32_t mx[NQ];
+  uint32_t accd[NQ][NACC];
+  int32_t hs[NQ][NACC];
+  int32_t inv[NQ];
 #pragma unroll
-  for (int u = 0; u < NACC; ++u) accd[u] = 0;
-  int32_t hs[NACC];
+  for (int qi = 0; qi < NQ; ++qi) {
+    mx[qi] = -32768;
+    inv[qi] = 0;
 #pragma unroll
-  for (int u = 0; u < NACC; ++u) hs[u] = 0;
-  int32_t inv = 0;
+    for (int u = 0; u < NACC; ++u) accd[qi][u] = 0, hs[qi][u] = 0;
+  }
   bool any_hi = false;
-  v4i qv = v4i{0, 0, 0, 0};
 
   // row maximum, P and its sum once every score is in sS
   auto form_p = [&]() {
-    mx = wave_max_dpp(mx);
-    if (lane == 0) sRed[wave] = mx;
-    lds_barrier();
-    int32_t rowmax = sRed[0];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) rowmax = max(rowmax, sRed[w]);
-    const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
-    uint32_t psum = 0, hi = 0;
-    for (int j = tid; j < nK * CH; j += 64 * NW) {
-      uint32_t p = 0;
-      // x_sub = qk - rmp1 modulo 2^16
-      if (j < Tk) p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)sS[j] - rmp1), a.frac_bits);
-      sP[j] = (uint8_t)p;
-      psum += p;
-      hi |= p;
+    for (int qi = 0; qi < NQ; ++qi) {
+      mx[qi] = wave_max_dpp(mx[qi]);
+      if (lane == 0) sRed[qi][wave] = mx[qi];
     }
-    psum = wave_sum_dpp(psum);
-    if (lane == 0) sSum[wave] = psum;
+    lds_barrier();
+    uint32_t hi = 0;
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      int32_t rowmax = sRed[qi][0];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) rowmax = max(rowmax, sRed[qi][w]);
+      const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
+      uint32_t psum = 0;
+      for (int j = tid; j < nK * CH; j += 64 * NW) {
+        uint32_t p = 0;
+        // x_sub = qk - rmp1 modulo 2^16
+        if (j < Tk)
+          p = shift_exp_one((int32_t)(int16_t)(uint16_t)((uint32_t)sS[qi * MAXK + j] - rmp1), a.frac_bits);
+        sP[qi * MAXK + j] = (uint8_t)p;
+        psum += p;
+        hi |= p;
+      }
+      psum = wave_sum_dpp(psum);
+      if (lane == 0) sSum[qi][wave] = psum;
+    }
     if (hi & 0x80u) atomicOr(&sHi, 1u);
     lds_barrier();
-    uint32_t total = 0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) total += sSum[w];
-    inv = fisr((int32_t)total, a.rsqrt_off);
+    for (int qi = 0; qi < NQ; ++qi) {
+      uint32_t total = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) total += sSum[qi][w];
+      inv[qi] = fisr((int32_t)total, a.rsqrt_off);
+    }
     any_hi = sHi != 0;
   };
 
@@ -971,8 +1003,8 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   }
   for (int i = 0; i < T; ++i) {
     wait_vm_upto<NR - 2, DPC>(min(NR - 2, T - 1 - i));
-    if (i == 0) {
-      qv = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * SLOT + wave * WB + lane * 16);
+    if (NQ == 1 && i == 0) {
+      qv[0] = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * SLOT + wave * WB + lane * 16);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // q is read before its slot refills
     }
     v4i x[DPC];
@@ -984,16 +1016,19 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
     if (i < nK) {
 #pragma unroll
       for (int u = 0; u < DPC; ++u) {
-        int32_t acc = __builtin_amdgcn_sdot4(qv[0], x[u][0], 0, false);
-        acc = __builtin_amdgcn_sdot4(qv[1], x[u][1], acc, false);
-        acc = __builtin_amdgcn_sdot4(qv[2], x[u][2], acc, false);
-        acc = __builtin_amdgcn_sdot4(qv[3], x[u][3], acc, false);
-        acc = quad_sum_dpp(acc);  // the key's four 16-byte pieces
         const int j = i * CH + kkey + 16 * u;
-        if (j < Tk) {
-          const int32_t h16 = qk_requant16(acc, a.qk_m, a.qk_s);
-          if (cq == 0) sS[j] = (int16_t)h16;
-          mx = max(mx, h16);
+#pragma unroll
+        for (int qi = 0; qi < NQ; ++qi) {
+          int32_t acc = __builtin_amdgcn_sdot4(qv[qi][0], x[u][0], 0, false);
+          acc = __builtin_amdgcn_sdot4(qv[qi][1], x[u][1], acc, false);
+          acc = __builtin_amdgcn_sdot4(qv[qi][2], x[u][2], acc, false);
+          acc = __builtin_amdgcn_sdot4(qv[qi][3], x[u][3], acc, false);
+          acc = quad_sum_dpp(acc);  // the key's four 16-byte pieces
+          if (j < Tk) {
+            const int32_t h16 = qk_requant16(acc, a.qk_m, a.qk_s);
+            if (cq == 0) sS[qi * MAXK + j] = (int16_t)h16;
+            mx[qi] = max(mx[qi], h16);
+          }
         }
       }
       if (i == nK - 1) form_p();
@@ -1003,41 +1038,50 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
         const uint32_t pw = *reinterpret_cast<const uint32_t *>(sP + (i - nK) * CH + (vq0 + 4 * u) * 4);
         if (!any_hi) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) accd[j] = (uint32_t)__builtin_amdgcn_sdot4((int)pw, x[u][j], (int)accd[j], false);
+          for (int j = 0; j < 4; ++j)
+            accd[0][j] = (uint32_t)__builtin_amdgcn_sdot4((int)pw, x[u][j], (int)accd[0][j], false);
         } else {
           // P = 128 only after an int16 row-max wrap: split off the top bit
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            accd[j] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw & 0x7f7f7f7fu), x[u][j], (int)accd[j], false);
-            hs[j] = __builtin_amdgcn_sdot4((int)((pw >> 7) & 0x01010101u), x[u][j], hs[j], false);
+            accd[0][j] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw & 0x7f7f7f7fu), x[u][j], (int)accd[0][j], false);
+            hs[0][j] = __builtin_amdgcn_sdot4((int)((pw >> 7) & 0x01010101u), x[u][j], hs[0][j], false);
           }
         }
       }
     } else {
-      const uint4 pv = *reinterpret_cast<const uint4 *>(sP + (i - nK) * CH + vp * 16);
-      const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-      for (int u = 0; u < DPC; ++u) {
-        if (!any_hi) {
+      for (int qi = 0; qi < NQ; ++qi) {
+        const uint4 pv = *reinterpret_cast<const uint4 *>(sP + qi * MAXK + (i - nK) * CH + vp * 16);
+        const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            accd[u] = (uint32_t)__builtin_amdgcn_sdot4((int)pw[e], x[u][e], (int)accd[u], false);
-        } else {
-          // P = 128 only after an int16 row-max wrap: split off the top bit
+        for (int u = 0; u < DPC; ++u) {
+          if (!any_hi) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            accd[u] = (uint32_t)__builtin_amdgcn_sdot4((int)(pw[e] & 0x7f7f7f7fu), x[u][e], (int)accd[u], false);
-            hs[u] = __builtin_amdgcn_sdot4((int)((pw[e] >> 7) & 0x01010101u), x[u][e], hs[u], false);
+            for (int e = 0; e < 4; ++e)
+              accd[qi][u] = (uint32_t)__builtin_amdgcn_sdot4((int)pw[e], x[u][e], (int)accd[qi][u], false);
+          } else {
+            // P = 128 only after an int16 row-max wrap: split off the top bit
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              accd[qi][u] =
+                  (uint32_t)__builtin_amdgcn_sdot4((int)(pw[e] & 0x7f7f7f7fu), x[u][e], (int)accd[qi][u], false);
+              hs[qi][u] = __builtin_amdgcn_sdot4((int)((pw[e] >> 7) & 0x01010101u), x[u][e], hs[qi][u], false);
+            }
           }
         }
       }
     }
   }
-  auto store = [&](uint32_t v, int d) {
-    int32_t y = rshift((int32_t)(v * (uint32_t)inv), a.rsqrt_off);
-    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv), a.rsqrt_off);
+  auto store = [&](uint32_t v, int d, int qi) {
+    int32_t y = rshift((int32_t)(v * (uint32_t)inv[qi]), a.rsqrt_off);
+    y = rshift((int32_t)((uint32_t)y * (uint32_t)inv[qi]), a.rsqrt_off);
     y = rshift((int32_t)((uint32_t)y * a.av_m), a.av_s);
-    a.out[decode_out_index(a, b, h * D + d)] = (int8_t)clampi(y, -127, 127);
+    const int8_t o = (int8_t)clampi(y, -127, 127);
+    if constexpr (NQ == 1)
+      a.out[decode_out_index(a, b, h * D + d)] = o;
+    else if (qi < a.Tq)
+      a.out[b * a.o_sb + (int64_t)qi * a.o_st + h * D + d] = o;
   };
   if (VQ) {
     // lanes l and l ^ 16, l ^ 32 hold other quads of the same d; then the
@@ -1046,7 +1090,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
     uint32_t *vw = &v.x;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t t = accd[j] + ((uint32_t)hs[j] << 7);
+      uint32_t t = accd[0][j] + ((uint32_t)hs[0][j] << 7);
       t += (uint32_t)__shfl_xor((int)t, 16);
       vw[j] = t + (uint32_t)__shfl_xor((int)t, 32);
     }
@@ -1057,18 +1101,20 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
       uint32_t t = 0;
 #pragma unroll
       for (int w = 0; w < NW; ++w) t += sPart[w * 64 + tid];
-      store(t, tid);
+      store(t, tid, 0);
     }
   } else {
 #pragma unroll
-    for (int u = 0; u < DPC; ++u) {
-      // the row's LPR lanes l .. l + LPR - 1 (l % LPR == 0): quad sums, then
-      // row_shl:4 / :8 (lane i reads lane i + n of its 16-lane row) into l
-      int32_t v = quad_sum_dpp((int32_t)(accd[u] + ((uint32_t)hs[u] << 7)));
-      if (LPR >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, true);
-      if (LPR >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0xf, true);
-      if (vp == 0) store((uint32_t)v, vrow + u * RPD);
-    }
+    for (int qi = 0; qi < NQ; ++qi)
+#pragma unroll
+      for (int u = 0; u < DPC; ++u) {
+        // the row's LPR lanes l .. l + LPR - 1 (l % LPR == 0): quad sums, then
+        // row_shl:4 / :8 (lane i reads lane i + n of its 16-lane row) into l
+        int32_t v = quad_sum_dpp((int32_t)(accd[qi][u] + ((uint32_t)hs[qi][u] << 7)));
+        if (LPR >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x104, 0xf, 0xf, true);
+        if (LPR >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x108, 0xf, 0xf, true);
+        if (vp == 0) store((uint32_t)v, vrow + u * RPD, qi);
+      }
   }
 }
 
@@ -1407,6 +1453,29 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
 int launch_attn_decode(const AttnArgs &a, hipStream_t s) {
   if ((int64_t)a.B * a.H * a.Tq == 0) return 0;
   if (a.Tk > DEC_MAX_TK) return fail("decode attention supports at most 4096 keys");
+  // head_dim 64, no mask, 16-byte aligned operands, at most 2048 keys: the
+  // streaming kernel, the query positions of a head sharing its K/V stream
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.vt) |
+                       reinterpret_cast<uintptr_t>(a.q) | (uintptr_t)a.k_st | (uintptr_t)a.k_sh |
+                       (uintptr_t)a.k_sb | (uintptr_t)a.v_sd | (uintptr_t)a.v_sh | (uintptr_t)a.v_sb |
+                       (uintptr_t)a.q_sb | (uintptr_t)a.q_st;
+  if (a.D == 64 && !a.mask && (al & 15) == 0 && a.Tk <= 2048 && a.v_sq == 4) {
+    AttnArgs c = a;
+    c.max_tk = a.Tk;
+    c.o_frag_kp = 0;
+    const dim3 grid((unsigned)(a.B * a.H));
+#define IW_DQ(NQ_) \
+  hipLaunchKernelGGL((attn_decode_stream_kernel<2048, IW_DS_NR, IW_DS_CH, 4, false, NQ_>), grid, dim3(256), 0, s, c, \
+                     nullptr)
+    if (a.Tq <= 2)
+      IW_DQ(2);
+    else if (a.Tq <= 4)
+      IW_DQ(4);
+    else
+      IW_DQ(8);
+#undef IW_DQ
+    return check_launch("attn_decode_stream_kernel");
+  }
   hipLaunchKernelGGL(attn_decode_kernel, dim3((unsigned)(a.B * a.H), (unsigned)a.Tq), dim3(256), 0,
                      s, a);
   return check_launch("attn_decode_kernel");

@@ -446,15 +446,13 @@ class DecoderRunner:
         s = att._scalars()
         H, D, Ta = self.H, self.D, self.Ta
         if Tq <= 8:
-            # one query position at a time over the cached K/V: the streaming
-            # decode kernel reads them once per position, where the prefill
-            # kernel would do the work of a whole 128-row query tile
-            for i in range(Tq):
-                _lib.call("iw_attention_decode_cache", q_ptr + i * q_st, q_sb, self.k_cross[l].data_ptr(),
-                          H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
-                          D * self.ta16, self.ta16, 4, out.data_ptr() + i * self.C, Tq * self.C, self.B, H, D,
-                          Ta, None, Ta, s["qm"], s["qs"], s["f"], s["am"], s["as_"], att.rsqrt_offset,
-                          _stream())
+            # the streaming decode kernel with every query position of a head
+            # sharing its pass over the cached K/V, where the prefill kernel
+            # would do the work of a whole 128-row query tile
+            _lib.call("iw_attention", q_ptr, q_sb, q_st, self.k_cross[l].data_ptr(), H * Ta * D, Ta * D, D,
+                      self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16, out.data_ptr(),
+                      Tq * self.C, self.C, None, self.B, H, Tq, Ta, D, s["qm"], s["qs"], s["f"], s["am"],
+                      s["as_"], att.rsqrt_offset, None, True, _stream())
         else:
             _lib.call("iw_attention", q_ptr, q_sb, q_st, self.k_cross[l].data_ptr(), H * Ta * D,
                       Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16,

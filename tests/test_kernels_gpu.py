@@ -377,7 +377,11 @@ def test_attention_prefill_fused(iw, oracle, gpu, B, H, Tq, Tk, D, masked):
 
 
 @pytest.mark.parametrize("B,H,Tq,Tk,D", [(1, 1, 1, 1, 64), (2, 3, 1, 1500, 64), (2, 2, 3, 3, 64),
-                                         (1, 2, 1, 448, 96), (3, 4, 1, 17, 64), (1, 1, 2, 100, 128)])
+                                         (1, 2, 1, 448, 96), (3, 4, 1, 17, 64), (1, 1, 2, 100, 128),
+                                         # several query rows sharing the K/V stream (2, 4 and 8 at
+                                         # once), up to the 2048 keys of that path and past them
+                                         (2, 20, 3, 1500, 64), (3, 4, 4, 1500, 64), (2, 3, 5, 1500, 64),
+                                         (1, 2, 8, 2048, 64), (1, 2, 3, 2100, 64), (2, 2, 7, 129, 64)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_attention_decode_fused(iw, oracle, gpu, B, H, Tq, Tk, D, masked):
     _print_case("attention decode", B, H, Tq, Tk, D, masked)
