@@ -31,7 +31,7 @@ namespace {
 // skinny_store's per-tensor form computes it, stored when g.out is set, and
 // the tile's first maximum of row m, reduced over the 32 lanes that hold the
 // row's 32 columns (lanes 0-31 or 32-63 of a wave, column = lane % 32).
-// Padding columns (n >= N) take key 0; every lane takes part.
+// Padding columns (n >= N) take key 0; every lane of the 32 takes part.
 __device__ __forceinline__ void classifier_argmax_store(const GemmArgs &g, const ColParams &c, int m, int n,
                                                         int tile, bool valid, uint32_t a) {
   uint32_t key = 0;
@@ -40,9 +40,17 @@ __device__ __forceinline__ void classifier_argmax_store(const GemmArgs &g, const
     if (g.out) reinterpret_cast<int8_t *>(g.out)[(int64_t)m * g.ldc + n] = (int8_t)y;
     key = ((uint32_t)(y + 128) << 5) | (uint32_t)(31 - (n & 31));
   }
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) key = max(key, (uint32_t)__shfl_xor((int)key, o));
-  if ((threadIdx.x & 31) == 0 && m < (int)g.M) g.amax[(int64_t)m * g.amax_ld + tile] = (uint16_t)key;
+  // keys < 2^13: the 16-lane row maxima with DPP moves, then each 32-lane
+  // half adds its second row's (lanes 16 and 48, read as scalars)
+  int32_t k = (int32_t)key;
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, 0xB1, 0xf, 0xf, false));   // quad [1,0,3,2]
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, 0x4E, 0xf, 0xf, false));   // quad [2,3,0,1]
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  k = max(k, __builtin_amdgcn_update_dpp(0, k, 0x140, 0xf, 0xf, false));  // row_mirror
+  const int lane = threadIdx.x & 63;
+  const int32_t k16 = __builtin_amdgcn_readlane(k, 16), k48 = __builtin_amdgcn_readlane(k, 48);
+  k = max(k, lane < 32 ? k16 : k48);
+  if ((lane & 31) == 0 && m < (int)g.M) g.amax[(int64_t)m * g.amax_ld + tile] = (uint16_t)k;
 }
 
 // Each wave multiplies the block's 32 x 32 tile over SPW k32 steps; a block
