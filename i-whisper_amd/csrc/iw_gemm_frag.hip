@@ -152,8 +152,7 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_frag_kernel(GemmArgs g, Skinny
     const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
     atomicAdd(&sTile[row * PLD + (lane & 31)], (int32_t)((uint32_t)acc[0][r] + (uint32_t)acc[1][r]));
   }
-  xs += __shfl_xor(xs, 32);
-  if (lane < 32) atomicAdd(&sXs[lane], xs);
+  atomicAdd(&sXs[lane & 31], xs);  // lanes l and l + 32 hold halves of row l % 32
   if (GELU && tid < 16) sLut[tid] = (uint8_t)lutv;
   __syncthreads();
 
