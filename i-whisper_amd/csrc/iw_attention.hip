@@ -797,39 +797,6 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 // loaded into registers behind the first chunks' copies.
 // ---------------------------------------------------------------------------
 
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// s_waitcnt vmcnt(n * F) for a run-time n in [0, N]
-template <int N, int F>
-__device__ __forceinline__ void wait_vm_upto(int n) {
-  if (n >= N) {
-    wait_vm<N * F>();
-  } else if constexpr (N > 0) {
-    wait_vm_upto<N - 1, F>(n);
-  }
-}
-
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// global_load_lds_dwordx4: lane l copies 16 bytes from src to LDS byte
-// address lds + 16 l. Inline assembly, so that the compiler adds no waits.
-__device__ __forceinline__ void dma16_lds(const int8_t *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// the LDS part of a barrier: this wave's LDS writes are done, then all waves
-// meet (without __syncthreads' release fence, which would drain the copies)
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // 128-key chunks in a 3-slot ring (24 KB): measured fastest among chunks of
 // 64 / 128 / 256 keys and rings of 2 to 10 slots (several small blocks per CU
 // hide each block's row-maximum pause better than one deep ring).

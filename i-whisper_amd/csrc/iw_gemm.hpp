@@ -179,6 +179,11 @@ __device__ inline void frag_prefetch_keep(const uint32_t (&v)[NL]) {
 // a and b fragment-major with padded K = frag_kpad(K); out_frag: the int8
 // output is itself written fragment-major (padded K = frag_kpad(N)).
 int gemm_frag(const GemmArgs &g, const SkinnyScatter *scatter, bool out_frag, hipStream_t s);
+// The classifier (EPI_S8, optionally with amax) as one persistent block per
+// CU streaming the weight tiles (iw_classifier_stream.hip): M <= 128,
+// Kp in {640, 960, 1280}, at least two column tiles per CU.
+bool classifier_stream_eligible(const GemmArgs &g);
+int classifier_stream(const GemmArgs &g, hipStream_t s);
 int launch_frag_pack(const int8_t *src, int64_t rows, int64_t cols, int64_t ld, int8_t *dst, hipStream_t s);
 
 // Rows from which the 256 x 128 tile kernel (iw_gemm_big.hip) is used.

@@ -46,18 +46,6 @@ constexpr int NT = 64 * NWAVES;
 constexpr int GROUP_M = 4;
 constexpr int XCDS = 8;
 
-// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4): the wave
-// writes 1 KB at LDS byte address `lds` (lane l at lds + 16 l). Issued as
-// inline assembly so that the compiler does not add waits for it: the loop
-// below waits on vmcnt itself. No kernel using it keeps a value in M0.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const int8_t *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
 // Fourth word of a raw buffer resource on gfx9-family GPUs (32-bit data
 // format; offsets range-checked against the record count).
 constexpr int kBufferFlags = 0x00020000;
@@ -212,9 +200,9 @@ void gemm_dtl_kernel(GemmArgs g, int tiles_n, int tiles_total, int per_xcd) {
     const int st = kt % STAGES;
     const int k0 = min(kt, nk - 1) * BK;
     if (c < ACP)
-      dma16(ga[c] + k0, ldsA + st * A_STAGE + c * 1024);
+      dma16_lds(ga[c] + k0, ldsA + st * A_STAGE + c * 1024);
     else
-      dma16(gb[c - ACP] + k0, ldsB + st * B_STAGE + (c - ACP) * 1024);
+      dma16_lds(gb[c - ACP] + k0, ldsB + st * B_STAGE + (c - ACP) * 1024);
   };
   auto issue = [&](int kt) {
 #pragma unroll

@@ -262,10 +262,12 @@ int gemm_frag(const GemmArgs &g, const SkinnyScatter *scatter, bool out_frag, hi
       if (gelu) return launch_frag<EPI_L8, true, false, false>(g, sc, s);
       return launch_frag<EPI_L8, false, false, false>(g, sc, s);
     case EPI_L32RES: return launch_frag<EPI_L32RES, false, false, false>(g, sc, s);
-    case EPI_S8:
+    case EPI_S8: {
       if (gelu || out_frag) return fail("the fragment-major classifier has a plain per-tensor epilogue");
+      if (classifier_stream_eligible(g)) return classifier_stream(g, s);
       if (g.amax) return launch_frag<EPI_S8, false, false, false, true>(g, sc, s);
       return launch_frag<EPI_S8, false, false, false>(g, sc, s);
+    }
     default: return fail("the fragment-major GEMM has Linear8, Linear32 + residual15 and classifier epilogues");
   }
 }

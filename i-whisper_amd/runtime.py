@@ -9,8 +9,10 @@ chosen for the MI355X instead of the reference's per-call tensors:
 * The residual stream is one int16 buffer updated in place by the fused
   Linear32 + residual15 kernels.
 * The decoder keeps preallocated per-head KV caches: self-attention K as
-  [B, H, n_ctx, D] and V transposed per head [B, H, D, n_ctx16];
-  cross-attention K/V likewise, projected once per utterance. This replaces
+  [B, H, n_ctx, D] and V in key quads [B, H, n_ctx16 / 4, D, 4] (head_dim 64;
+  V transposed per head [B, H, D, n_ctx16] for other head sizes);
+  cross-attention K as [B, H, n_audio_ctx, D] and V transposed per head,
+  projected once per utterance. This replaces
   the reference's hook-based ``torch.cat`` cache (model_int.py:1587-1618) with
   identical values.
 * Greedy decoding feeds the last token each step (decoding.py:148-179,

@@ -136,7 +136,8 @@ def test_linear32_residual15_frag(iw, oracle, gpu, M, K, N):
     assert np.array_equal(host(rt), exp)
 
 
-@pytest.mark.parametrize("M,K,N", [(128, 1280, 51865), (1, 384, 51865), (3, 512, 1000)])
+@pytest.mark.parametrize("M,K,N", [(128, 1280, 51865), (1, 384, 51865), (3, 512, 1000), (64, 512, 20000),
+                                   (97, 768, 17000)])
 def test_classifier_frag(iw, oracle, gpu, M, K, N):
     print("case: classifier_frag", M, K, N, flush=True)
     r = gen.rng(M + K + N)

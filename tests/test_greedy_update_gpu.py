@@ -34,7 +34,10 @@ def tile_maxima(logits):
     return (((val + 128) << 5) | (31 - col)).astype(np.uint16)
 
 
-@pytest.mark.parametrize("M,K,N", [(128, 1280, 51865), (3, 512, 1000), (1, 384, 51865), (40, 768, 70)])
+# (128, 1280, 51865), (1, 384, 51865), (77, 768, 20000), (33, 1280, 51865) and (100, 1024, 17000) take
+# the streaming kernel (at least two column tiles per CU; Kp = 640, 960 and 1280, partial m-subtiles)
+@pytest.mark.parametrize("M,K,N", [(128, 1280, 51865), (3, 512, 1000), (1, 384, 51865), (40, 768, 70),
+                                   (77, 768, 20000), (33, 1280, 51865), (100, 1024, 17000)])
 def test_classifier_argmax_frag(iw, oracle, gpu, M, K, N):
     print("case: classifier_argmax_frag", M, K, N, flush=True)
     r = gen.rng(M + K + N + 1)
