@@ -75,6 +75,9 @@ SIGNATURES = {
                                   _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "iw_layernorm32_frag": [_p, _p, _p, _u8, _i8, _u32, _i8, _u32, _p, _i64, _i64, _b, _p, _i64, _i64,
                             _p],
+    "iw_attention_decode_cross_lnq": [_p, _i64, _p, _p, _u8, _i8, _u32, _i8, _u32, _b, _p, _p, _p, _p, _p, _b, _b,
+                                      _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64,
+                                      _u8, _i8, _i32, _u8, _i8, _u32, _p],
     "iw_attention_decode_cache_frag": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p,
                                        _i64, _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32,
                                        _p],

@@ -958,6 +958,83 @@ int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *
                                       av_multiplier, av_shift, rsqrt_offset, true, stream);
 }
 
+int iw_attention_decode_cross_lnq(const int16_t *x, int64_t x_ld, const int8_t *ln_weight, const int32_t *ln_bias,
+                                  uint8_t ln_multiplier, int8_t ln_shift, uint32_t ln_out_multiplier,
+                                  int8_t ln_out_shift, uint32_t ln_rsqrt_offset, bool ln_has_bias,
+                                  const int8_t *q_weight, const int32_t *q_bias, const int8_t *q_weight_zero,
+                                  const uint32_t *q_multiplier, const int8_t *q_shift, bool q_has_bias,
+                                  bool q_asymmetric, const int8_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                  const int8_t *vt, int64_t v_sb, int64_t v_sh, int64_t v_sd, int8_t *out,
+                                  int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
+                                  uint8_t qk_multiplier, int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
+                                  int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream) {
+  IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
+  IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
+  IW_REQUIRE(head_dim == 64, "the fused cross-attention takes head_dim 64");
+  const int64_t C = heads * head_dim;
+  const int code = layernorm_width_code(C);
+  IW_REQUIRE(code >= 0, "unsupported LayerNorm hidden size: " + std::to_string(C));
+  IW_REQUIRE(batch >= 0 && batch <= kSkinnyMaxRows && k_length > 0 && k_length <= 2048,
+             "the fused cross-attention takes at most 128 rows and 1 .. 2048 keys");
+  IW_REQUIRE(x_ld >= C, "x_ld must be at least heads * head_dim");
+  IW_REQUIRE(v_sd % 16 == 0 && v_sd >= ((k_length + 15) / 16) * 16,
+             "transposed V rows must be 16-byte multiples covering k_length");
+  if (batch == 0) return IW_OK;
+  IW_REQUIRE(x && ln_weight && q_weight && q_multiplier && q_shift && k && vt && out, "null tensor pointer");
+  IW_REQUIRE(!ln_has_bias || ln_bias, "ln_has_bias set but ln_bias is null");
+  IW_REQUIRE(!q_has_bias || q_bias, "q_has_bias set but q_bias is null");
+  IW_REQUIRE(!q_asymmetric || q_weight_zero, "q_asymmetric set but q_weight_zero is null");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q_weight) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(vt) | (uintptr_t)k_sb | (uintptr_t)k_sh | (uintptr_t)k_st |
+                          (uintptr_t)v_sb | (uintptr_t)v_sh;
+  IW_REQUIRE((align & 15) == 0, "decode attention operands must be 16-byte aligned");
+  IW_REQUIRE((reinterpret_cast<uintptr_t>(x) & 1) == 0, "x must be 2-byte aligned");
+  AttnArgs a;
+  a.k = k;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.k_st = k_st;
+  a.vt = vt;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.v_sd = v_sd;
+  a.v_sq = 4;
+  a.vt_ld = v_sd;
+  a.out = out;
+  a.B = (int32_t)batch;
+  a.H = (int32_t)heads;
+  a.Tq = 1;
+  a.Tk = (int32_t)k_length;
+  a.D = (int32_t)head_dim;
+  a.qk_m = qk_multiplier;
+  a.qk_s = (uint32_t)(qk_shift > 0 ? qk_shift : 0);
+  a.frac_bits = frac_bits;
+  a.av_m = av_multiplier;
+  a.av_s = (uint32_t)(av_shift < 0 ? 0 : (av_shift > 32 ? 32 : av_shift));
+  a.rsqrt_off = rsqrt_offset;
+  a.max_tk = (int32_t)k_length;
+  a.o_frag_kp = frag_kpad(C);
+  LnQueryArgs lq;
+  lq.x = x;
+  lq.ldx = x_ld;
+  lq.gamma = ln_weight;
+  lq.beta = ln_has_bias ? ln_bias : nullptr;
+  lq.ln_m = ln_multiplier;
+  lq.ln_s = ln_shift;
+  lq.out_m = ln_out_multiplier;
+  lq.out_s = ln_out_shift;
+  lq.rsqrt_off = ln_rsqrt_offset;
+  lq.code = code;
+  lq.hidden = (int32_t)C;
+  lq.wq = q_weight;
+  lq.kp = frag_kpad(C);
+  lq.bias = q_has_bias ? q_bias : nullptr;
+  lq.wz = q_asymmetric ? q_weight_zero : nullptr;
+  lq.mult = q_multiplier;
+  lq.shift = q_shift;
+  return launch_attn_decode_cross_lnq(a, lq, as_stream(stream));
+}
+
 int iw_classifier_argmax_frag(const int8_t *x, const int8_t *weight, uint32_t multiplier, int8_t shift,
                               int8_t *out, uint16_t *row_max, int64_t M, int64_t K, int64_t N,
                               iw_stream_t stream) {

@@ -827,8 +827,165 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 #define IW_DSELF_NW 4
 #endif
 
-template <int MAXK, int NR, int CH, int NW = 4, bool VQ = false, int NQ = 1>
-__global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
+// The query of (batch b, head h) for attn_decode_cross_lnq_kernel, as 64
+// bytes of LDS: LayerNorm32 of row b (the integer steps of
+// layernorm32_row_kernel: thread t owns elements t, t + 256, ..., three
+// reduction rounds) into the LDS row hb, then Linear8 of the head's 64
+// channels: wave w takes the k32 steps s = w, w + 4, ... of both 32-channel
+// fragment rows of wq (lane l: channel 32 r + l % 32, bytes 32 s + 16 (l / 32)
+// .. +15, against the same bytes of hb), the partial sums meet in LDS
+// (ds_add, modulo 2^32) and threads 0-63 apply the Linear8 epilogue with the
+// row sum of hb for the zero-point term. The row, the parameters and the
+// first five steps' weight fragments are requested first (ln_query_load),
+// ahead of the block's first K/V chunk copies, so that the LayerNorm waits
+// for its own loads only; the other five steps' fragments after it.
+struct LnqRegs {
+  int32_t v[5], gm[5], bt[5];
+  int32_t qb, qz, qs;
+  uint32_t qm;
+  v4i f0[5], f1[5];
+};
+
+__device__ __forceinline__ void lnq_frags(const LnQueryArgs &lq, int h, int half, v4i (&f0)[5], v4i (&f1)[5]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nst = (int)(lq.kp >> 5);  // k32 steps (the padding has zero weights)
+  const int8_t *w0 = lq.wq + ((int64_t)(2 * h) * nst) * 1024 + lane * 16;
+  const int8_t *w1 = w0 + (int64_t)nst * 1024;
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const int st = wave + 4 * (5 * half + t);
+    const int sc = st < nst ? st : 0;
+    f0[t] = *reinterpret_cast<const v4i *>(w0 + (int64_t)sc * 1024);
+    f1[t] = *reinterpret_cast<const v4i *>(w1 + (int64_t)sc * 1024);
+  }
+}
+
+__device__ __forceinline__ void ln_query_load(const LnQueryArgs &lq, int64_t b, int h, LnqRegs &r) {
+  const int tid = threadIdx.x;
+  const int C = lq.hidden;
+  const int16_t *xr = lq.x + b * lq.ldx;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const int e = tid + 256 * j;
+    const bool ok = e < C;
+    r.v[j] = ok ? xr[e] : 0;
+    r.gm[j] = ok ? lq.gamma[e] : 0;
+    r.bt[j] = (ok && lq.beta) ? lq.beta[e] : 0;
+  }
+  // the epilogue parameters of channel h * 64 + tid % 64
+  const int n = h * 64 + (tid & 63);
+  r.qb = lq.bias ? lq.bias[n] : 0;
+  r.qz = lq.wz ? (int32_t)lq.wz[n] : 0;
+  r.qm = lq.mult[n];
+  r.qs = lq.shift[n];
+  lnq_frags(lq, h, 0, r.f0, r.f1);
+}
+
+// The normalised row (up to 1280 bytes) and the query sums (64 words) use
+// sP, which the attention first writes after the scores.
+__device__ __forceinline__ const int8_t *ln_query(const LnQueryArgs &lq, LnqRegs &r, int h, uint8_t *sP) {
+  constexpr int NWV = 4;
+  __shared__ uint32_t sLn[3][NWV];  // the LayerNorm's wave partials
+  __shared__ __attribute__((aligned(16))) int8_t q8[64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int C = lq.hidden;
+  int8_t *hb = reinterpret_cast<int8_t *>(sP);
+  int32_t *qacc = reinterpret_cast<int32_t *>(sP + 1280);
+  if (r.qs < 0 || r.qs >= 32) r.qm = 0, r.qs = 0;  // linear8_scalar.cpp:71-74: such a shift gives 0
+  if (tid < 64) qacc[tid] = 0;
+
+  uint32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) sum += (uint32_t)r.v[j];
+  sum = wave_sum_dpp(sum);
+  if (lane == 0) sLn[0][wave] = sum;
+  lds_barrier();
+  const int32_t mean = norm_reduce((int32_t)(sLn[0][0] + sLn[0][1] + sLn[0][2] + sLn[0][3]), lq.code);
+  int32_t maxsq = 0;
+#pragma unroll
+  for (int j = 0; j < 5; ++j)
+    if (tid + 256 * j < C) {
+      const int32_t d = r.v[j] - mean;
+      maxsq = max(maxsq, (int32_t)((uint32_t)d * (uint32_t)d));
+    }
+  maxsq = wave_max_dpp(maxsq);
+  if (lane == 0) sLn[1][wave] = (uint32_t)maxsq;
+  lds_barrier();
+  maxsq = max(max((int32_t)sLn[1][0], (int32_t)sLn[1][1]), max((int32_t)sLn[1][2], (int32_t)sLn[1][3]));
+  int32_t rs = bitlen(maxsq) - 16;
+  rs = rs < 0 ? 0 : rs;
+  rs = (rs + 1) & ~1;
+  uint32_t vs = 0;
+#pragma unroll
+  for (int j = 0; j < 5; ++j)
+    if (tid + 256 * j < C) {
+      const int32_t d = r.v[j] - mean;
+      vs += (uint32_t)rshift((int32_t)((uint32_t)d * (uint32_t)d), (uint32_t)rs);
+    }
+  vs = wave_sum_dpp(vs);
+  if (lane == 0) sLn[2][wave] = vs;
+  lds_barrier();
+  const int32_t var = norm_reduce((int32_t)(sLn[2][0] + sLn[2][1] + sLn[2][2] + sLn[2][3]), lq.code);
+  const int32_t inv = fisr(var, lq.rsqrt_off);
+  const uint32_t nshift = (uint32_t)(lq.ln_s + (rs >> 1));
+  uint32_t rsum = 0;
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const int e = tid + 256 * j;
+    if (e < C) {
+      const int32_t d = r.v[j] - mean;
+      const uint32_t t = (uint32_t)d * (uint32_t)inv * lq.ln_m;
+      const int32_t y = clampi(rshift((int32_t)t, nshift), -16383, 16383);
+      const uint32_t av = (uint32_t)y * (uint32_t)r.gm[j] + (uint32_t)r.bt[j];
+      const int32_t yo = clampi(rshift(mulh((int32_t)av, lq.out_m), (uint32_t)lq.out_s), -127, 127);
+      hb[e] = (int8_t)yo;
+      rsum += (uint32_t)yo;
+    }
+  }
+  // the normalised row's sum, for the zero-point term (round 0's words are
+  // free: every thread read them before the second barrier)
+  rsum = wave_sum_dpp(rsum);
+  if (lane == 0) sLn[0][wave] = rsum;
+  lds_barrier();
+
+  const int nst = (int)(lq.kp >> 5);
+  const int hoff = 16 * (lane >> 5);
+  int32_t acc0 = 0, acc1 = 0;
+  auto dot = [&](int half, const v4i (&f0)[5], const v4i (&f1)[5]) {
+#pragma unroll
+    for (int t = 0; t < 5; ++t) {
+      const int st = wave + NWV * (5 * half + t);
+      if (st < nst) {
+        const v4i hv = *reinterpret_cast<const v4i *>(hb + 32 * st + hoff);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc0 = __builtin_amdgcn_sdot4(f0[t][e], hv[e], acc0, false);
+          acc1 = __builtin_amdgcn_sdot4(f1[t][e], hv[e], acc1, false);
+        }
+      }
+    }
+  };
+  // then steps 5..9 of each wave (kp <= 1280: at most ten per wave)
+  dot(0, r.f0, r.f1);
+  lnq_frags(lq, h, 1, r.f0, r.f1);
+  dot(1, r.f0, r.f1);
+  atomicAdd(&qacc[lane & 31], acc0);
+  atomicAdd(&qacc[32 + (lane & 31)], acc1);
+  lds_barrier();
+  if (tid < 64) {
+    const int32_t xsum = (int32_t)(sLn[0][0] + sLn[0][1] + sLn[0][2] + sLn[0][3]);
+    // acc - wz * rowsum + bias modulo 2^32 (|rowsum| <= 127 C < 2^23: exact
+    // in the 24-bit multiplier), then the Linear8 requantization
+    const uint32_t corr = (uint32_t)qacc[tid] - (uint32_t)__mul24(r.qz, xsum) + (uint32_t)r.qb;
+    q8[tid] = (int8_t)clampi(rshift(mulh((int32_t)corr, r.qm), (uint32_t)r.qs), -127, 127);
+  }
+  lds_barrier();
+  return q8;
+}
+
+template <int MAXK, int NR, int CH, int NW, bool VQ, int NQ, bool LNQ>
+__device__ __forceinline__ void attn_decode_stream_body(const AttnArgs &a, const int32_t *pos,
+                                                        const LnQueryArgs &lq) {
   constexpr int D = 64;
   constexpr int DPC = CH / (16 * NW);  // copies per wave per chunk
   constexpr int SLOT = 1024 * NW * DPC;  // bytes per ring slot (CH keys x 64 bytes)
@@ -840,6 +997,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   constexpr int NACC = VQ ? 4 : DPC;  // P.V sums per lane
   static_assert(!VQ || NW * 64 * 4 <= MAXK * 2, "the wave sums of P.V fit in the score array");
   static_assert(NQ == 1 || !VQ, "several queries stream V transposed");
+  static_assert(!LNQ || (NQ == 1 && !VQ && NW == 4 && MAXK >= 1280), "the fused query: one, V transposed");
   __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
   __shared__ __attribute__((aligned(16))) int16_t sS[NQ * MAXK];  // requantized scores
   __shared__ __attribute__((aligned(16))) uint8_t sP[NQ * MAXK];
@@ -893,14 +1051,18 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   // first, into the last ring slot (free until chunk NR - 1), so the chunk
   // waits cover it (counted as DPC copies: the waits below are in whole
   // chunks); several are loaded into registers after the first chunks.
-  if constexpr (NQ == 1) {
+  if constexpr (NQ == 1 && !LNQ) {
 #pragma unroll
     for (int u = 0; u < DPC; ++u)
       dma16_lds(a.q + b * a.q_sb + (int64_t)h * D + cq * 16, ring + (NR - 1) * SLOT + u * 1024);
   }
+  LnqRegs lr;
+  if constexpr (LNQ) ln_query_load(lq, b, h, lr);
 #pragma unroll
   for (int i = 0; i < NR - 1; ++i)
     if (i < T) issue(i);
+  const int8_t *q8 = nullptr;
+  if constexpr (LNQ) q8 = ln_query(lq, lr, h, sP);
   v4i qv[NQ];
   if constexpr (NQ > 1) {
 #pragma unroll
@@ -971,7 +1133,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
   for (int i = 0; i < T; ++i) {
     wait_vm_upto<NR - 2, DPC>(min(NR - 2, T - 1 - i));
     if (NQ == 1 && i == 0) {
-      qv[0] = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * SLOT + wave * WB + lane * 16);
+      if constexpr (LNQ)
+        qv[0] = *reinterpret_cast<const v4i *>(q8 + cq * 16);
+      else
+        qv[0] = *reinterpret_cast<const v4i *>(sRing + (NR - 1) * SLOT + wave * WB + lane * 16);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // q is read before its slot refills
     }
     v4i x[DPC];
@@ -1083,6 +1248,21 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a,
         if (vp == 0) store((uint32_t)v, vrow + u * RPD, qi);
       }
   }
+}
+
+template <int MAXK, int NR, int CH, int NW = 4, bool VQ = false, int NQ = 1>
+__global__ __launch_bounds__(64 * NW) void attn_decode_stream_kernel(AttnArgs a, const int32_t *pos) {
+  attn_decode_stream_body<MAXK, NR, CH, NW, VQ, NQ, false>(a, pos, LnQueryArgs());
+}
+
+// The decoder cross-attention with its query computed in the block: the
+// LayerNorm before the cross-attention (one row per block, 20 blocks per
+// row at Whisper-large) and the head's 64 query channels, while the first
+// K chunks are in flight; it replaces a LayerNorm and a query GEMM launch.
+// (five blocks per CU, as the plain kernel: at most 96 VGPRs)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void attn_decode_cross_lnq_kernel(
+    AttnArgs a, LnQueryArgs lq) {
+  attn_decode_stream_body<2048, IW_DS_NR, IW_DS_CH, 4, false, 1, true>(a, nullptr, lq);
 }
 
 // ---------------------------------------------------------------------------
@@ -1348,6 +1528,18 @@ int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s) {
   }
 #undef IW_PF
   return check_launch("attn_prefill_kernel");
+}
+
+int launch_attn_decode_cross_lnq(const AttnArgs &a, const LnQueryArgs &lq, hipStream_t s) {
+  if ((int64_t)a.B * a.H == 0) return 0;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.vt) | (uintptr_t)a.k_st |
+                       (uintptr_t)a.k_sh | (uintptr_t)a.k_sb | (uintptr_t)a.v_sd | (uintptr_t)a.v_sh |
+                       (uintptr_t)a.v_sb | reinterpret_cast<uintptr_t>(lq.wq);
+  if (a.D != 64 || (al & 15) != 0 || a.v_sq != 4 || a.max_tk != a.Tk || a.Tk > 2048 || lq.hidden != a.H * 64 ||
+      lq.hidden > 1280 || lq.kp > 1280 || lq.code < 0)
+    return fail("the fused cross-attention takes head_dim 64, V transposed, at most 2048 keys and 1280 channels");
+  hipLaunchKernelGGL(attn_decode_cross_lnq_kernel, dim3((unsigned)(a.B * a.H)), dim3(256), 0, s, a, lq);
+  return check_launch("attn_decode_cross_lnq_kernel");
 }
 
 int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s) {

@@ -52,6 +52,19 @@ __device__ __forceinline__ int8_t gelu_one(int32_t x, const uint8_t *lut, uint32
   return (int8_t)clampi(v, -127, 127);
 }
 
+// Division by the LayerNorm width as adds and floor shifts
+// (layernorm/layernorm_scalar.cpp:14-56), modulo 2^32; code 0..4 for the
+// widths 384, 512, 768, 1024, 1280.
+__device__ __forceinline__ int32_t norm_reduce(int32_t v, int code) {
+  switch (code) {
+    case 0: return (int32_t)((uint32_t)v + (uint32_t)(v >> 2) + (uint32_t)(v >> 3)) >> 9;
+    case 1: return v >> 9;
+    case 2: return (int32_t)((uint32_t)v + (uint32_t)(v >> 2) + (uint32_t)(v >> 3)) >> 10;
+    case 3: return v >> 10;
+    default: return (int32_t)((uint32_t)v + (uint32_t)(v >> 1)) >> 11;
+  }
+}
+
 // Integer fast inverse square root, two Newton steps
 // (layernorm/layernorm_scalar.cpp:309-438).
 __device__ __forceinline__ int32_t bitlen(int32_t v) { return v == 0 ? 0 : 32 - __clz(v); }

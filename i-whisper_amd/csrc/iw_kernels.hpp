@@ -40,6 +40,33 @@ struct AttnArgs {
   int64_t o_frag_kp = 0;         // decode over caches: > 0 writes out fragment-major [B][H*D]
 };
 
+// The LayerNorm and query projection that the fused decode cross-attention
+// (launch_attn_decode_cross_lnq) runs for its (batch, head) before the
+// attention: LayerNorm32 of residual row b (x + b * ldx, C = hidden int16)
+// with the LayerNorm's parameters, then the head's 64 query channels
+// h * 64 .. +63 of Linear8 over the fragment-major weight wq ([C][kp], kp =
+// frag_kpad(C)) with per-channel bias / weight zero point / multiplier /
+// shift (bias and wz may be null).
+struct LnQueryArgs {
+  const int16_t *x = nullptr;
+  int64_t ldx = 0;
+  const int8_t *gamma = nullptr;
+  const int32_t *beta = nullptr;
+  uint32_t ln_m = 0;
+  int32_t ln_s = 0;
+  uint32_t out_m = 0;
+  int32_t out_s = 0;
+  uint32_t rsqrt_off = 0;
+  int32_t code = 0;    // layernorm_width_code(hidden)
+  int32_t hidden = 0;
+  const int8_t *wq = nullptr;
+  int64_t kp = 0;
+  const int32_t *bias = nullptr;
+  const int8_t *wz = nullptr;
+  const uint32_t *mult = nullptr;
+  const int8_t *shift = nullptr;
+};
+
 int layernorm_width_code(int64_t h);
 // out_frag: out is the fragment-major image of [rows][hidden] (rows <= 128)
 int launch_layernorm32(const int16_t *x, const int8_t *gamma, const int32_t *beta, uint8_t ln_m,
@@ -115,5 +142,9 @@ int launch_attn_decode(const AttnArgs &a, hipStream_t s);
 // a.Tk + *pos (pos may be null). At most 4096 keys.
 constexpr int kDecodeCacheMaxKeys = 4096;
 int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s);
+// Decode cross-attention (one query per (batch, head), keys 0 .. a.Tk - 1,
+// V transposed, head_dim 64) whose query the kernel computes itself from
+// lq; a.q unused. a.o_frag_kp as for launch_attn_decode_cache.
+int launch_attn_decode_cross_lnq(const AttnArgs &a, const LnQueryArgs &lq, hipStream_t s);
 
 }  // namespace iw

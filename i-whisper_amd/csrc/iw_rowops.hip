@@ -10,18 +10,6 @@ namespace iw {
 
 namespace {
 
-// Division by the LayerNorm width as adds and floor shifts
-// (layernorm/layernorm_scalar.cpp:14-56), modulo 2^32.
-__device__ __forceinline__ int32_t norm_reduce(int32_t v, int code) {
-  switch (code) {
-    case 0: return (int32_t)((uint32_t)v + (uint32_t)(v >> 2) + (uint32_t)(v >> 3)) >> 9;
-    case 1: return v >> 9;
-    case 2: return (int32_t)((uint32_t)v + (uint32_t)(v >> 2) + (uint32_t)(v >> 3)) >> 10;
-    case 3: return v >> 10;
-    default: return (int32_t)((uint32_t)v + (uint32_t)(v >> 1)) >> 11;
-  }
-}
-
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += (uint32_t)__shfl_xor((int)v, o);

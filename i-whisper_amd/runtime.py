@@ -312,13 +312,15 @@ class DecoderRunner:
                  max_steps: Optional[int] = None, use_graph: bool = True,
                  filters: Optional[LogitFilters] = None, frag: bool = True, prefetch: bool = True,
                  eot: Optional[int] = None, logprobs: bool = True, no_speech: Optional[int] = None,
-                 sot_index: int = 0):
+                 sot_index: int = 0, fuse_cross: bool = True):
         """``eot``: the EOT id for GreedyDecoder.update's EOT freeze and the
         all-finished count without filters (the filters carry their own);
         ``logprobs``: accumulate each row's sum of log-probabilities
         (``sum_logprobs``); ``no_speech``: the no-speech token id, whose
         probability at the prompt position ``sot_index`` the prompt step
-        records (``no_speech_probs``)."""
+        records (``no_speech_probs``); ``fuse_cross``: the one-token step runs
+        each cross-attention's LayerNorm and query projection inside the
+        cross-attention kernel (head_dim 64), instead of as two launches."""
         self.dec = decoder
         self.B = batch
         C, H = decoder.n_state, decoder.n_head
@@ -361,6 +363,7 @@ class DecoderRunner:
         # each LayerNorm (and FC1) of the one-token step reads the next
         # GEMM's weight tiles into L2 (a hint; results do not depend on it)
         self.prefetch = prefetch
+        self.fuse_cross = fuse_cross and self.frag and self.D == 64 and n_audio_ctx <= 2048
         if self.frag:
             self.f_qkv = [_FragLinear(f) for f in self.self_qkv]
             self.f_out = [_FragLinear(b.attn.out) for b in decoder.blocks]
@@ -631,14 +634,25 @@ class DecoderRunner:
                       self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
                       blk.attn.rsqrt_offset, _stream())
             self.f_out[l].linear32_res(wvf, B, x16, sc["a"])
-            _ln_frag(blk.cross_attn_ln, x16, B, h8f, pf(self.f_cq[l]))
-            self.f_cq[l].linear8(h8f, B, q8)
             s = blk.cross_attn._scalars()
             Ta = self.Ta
-            _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_cross[l].data_ptr(),
-                      H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
-                      D * self.ta16, self.ta16, 4, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
-                      s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
+            if self.fuse_cross:
+                ln, cq = blk.cross_attn_ln, self.f_cq[l]
+                lsc = ln._scalars()
+                _lib.call("iw_attention_decode_cross_lnq", x16.data_ptr(), C, ln.weight.data_ptr(), _ptr(ln.bias),
+                          lsc["lm"], lsc["ls"], lsc["om"], lsc["os"], ln.offset, ln.bias is not None,
+                          cq.w.data_ptr(), _ptr(cq.bias), _ptr(cq.wz), cq.mult.data_ptr(), cq.shift.data_ptr(),
+                          cq.bias is not None, cq.wz is not None, self.k_cross[l].data_ptr(), H * Ta * D,
+                          Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16,
+                          wvf.data_ptr(), B, H, D, Ta, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
+                          blk.cross_attn.rsqrt_offset, _stream())
+            else:
+                _ln_frag(blk.cross_attn_ln, x16, B, h8f, pf(self.f_cq[l]))
+                self.f_cq[l].linear8(h8f, B, q8)
+                _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_cross[l].data_ptr(),
+                          H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
+                          D * self.ta16, self.ta16, 4, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
+                          s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
             self.f_co[l].linear32_res(wvf, B, x16, sc["c"])
             f1, f2 = self.f_fc1[l], self.f_fc2[l]
             _ln_frag(blk.mlp_ln, x16, B, h8f, pf(f1))

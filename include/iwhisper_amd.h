@@ -351,6 +351,32 @@ int iw_greedy_advance_filtered(const int8_t *logits, int64_t rows, int64_t cols,
  * (0 for cols > 5120 or a negative size). */
 int64_t iw_frag_bytes(int64_t rows, int64_t cols);
 
+/* The decode step's cross-attention with the LayerNorm and query projection
+ * before it fused in (model_int.py:1139-1145, cross_attn_ln then cross_attn,
+ * whose forward, :713-735, projects the query and attends over the cached
+ * K/V): each
+ * (batch b, head h) block normalises residual row b (x + b * x_ld, C =
+ * heads * 64 int16, LayerNorm32 with iw_layernorm32's parameters), projects
+ * it onto the head's 64 query channels (q_weight fragment-major [C][Kp],
+ * Linear8 parameters as iw_linear8) and attends as
+ * iw_attention_decode_cache_frag over k_length cached keys (V transposed:
+ * v_sq == 4). out is the fragment-major image of [batch][C], as
+ * iw_attention_decode_cache_frag writes it. Results equal iw_layernorm32 ->
+ * iw_linear8 -> iw_attention_decode_cache_frag; batch <= 128, head_dim 64,
+ * C in {384, 512, 768, 1024, 1280}, k_length <= 2048. No single counterpart
+ * in the reference, which runs the three calls. */
+int iw_attention_decode_cross_lnq(const int16_t *x, int64_t x_ld, const int8_t *ln_weight, const int32_t *ln_bias,
+                                  uint8_t ln_multiplier, int8_t ln_shift, uint32_t ln_out_multiplier,
+                                  int8_t ln_out_shift, uint32_t ln_rsqrt_offset, bool ln_has_bias,
+                                  const int8_t *q_weight, const int32_t *q_bias, const int8_t *q_weight_zero,
+                                  const uint32_t *q_multiplier, const int8_t *q_shift, bool q_has_bias,
+                                  bool q_asymmetric, const int8_t *k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                  const int8_t *vt, int64_t v_sb, int64_t v_sh, int64_t v_sd, int8_t *out,
+                                  int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
+                                  uint8_t qk_multiplier, int8_t qk_shift, int32_t frac_bits,
+                                  uint8_t av_multiplier, int8_t av_shift, uint32_t rsqrt_offset,
+                                  iw_stream_t stream);
+
 /* Row-major src [rows][cols] (row stride ld) to its fragment-major image,
  * padding included (dst holds iw_frag_bytes(rows, cols) bytes). */
 int iw_frag_pack(const int8_t *src, int64_t rows, int64_t cols, int64_t ld, int8_t *dst,

@@ -314,3 +314,92 @@ def test_weight_prefetch_does_not_change_results(iw, gpu, tiny_model):
                   for r in eager]
     assert np.array_equal(toks[0], toks[1])
     assert np.array_equal(logits[0], logits[1])
+
+
+def _unfrag(img, rows, cols):
+    """Row-major [rows, cols] from a fragment-major image (iwhisper_amd.h layout)."""
+    kp = (cols + 319) // 320 * 320
+    r = np.arange(rows)[:, None]
+    k = np.arange(cols)[None, :]
+    off = (r // 32) * 32 * kp + (k // 32) * 1024 + (r % 32 + 32 * ((k // 16) % 2)) * 16 + k % 16
+    return img[off]
+
+
+@pytest.mark.parametrize("B,H,Tk,bias,asym", [(2, 20, 1500, True, True), (5, 6, 1500, True, True),
+                                             (3, 12, 100, False, True), (1, 16, 7, True, False),
+                                             (128, 20, 1500, True, True)])
+def test_attention_decode_cross_lnq(iw, oracle, gpu, B, H, Tk, bias, asym):
+    """The cross-attention with the LayerNorm and query projection fused in
+    against the oracle chain layernorm32 -> linear8 -> attention: one row with
+    the full int16 range (|x - mean| > 46340: the per-element variance form),
+    query shifts outside [0, 31], every supported width."""
+    print("case: cross_lnq", B, H, Tk, bias, asym, flush=True)
+    D = 64
+    C = H * D
+    x, gamma, beta, lm, ls, om, os_ = gen.ln_case(B * 7 + H + Tk, B, C)
+    x[0, ::2], x[0, 1::2] = 32767, -32768
+    _, w, qb, qz, qm_, qs_ = gen.realistic_linear_case(B + C + Tk, 1, C, C, has_bias=bias, asym=asym)
+    qs_[:2] = [-1, 32]
+    q_, k, v, qm, qs, f, am, as_ = gen.attn_case(B + H + Tk + 1, B, H, 1, Tk, D)
+    h8 = oracle.layernorm32(x, gamma, beta, lm, ls, om, os_, 13)
+    q8 = oracle.linear8(h8, w, qb, qz, qm_, qs_)
+    exp = oracle.attention(np.ascontiguousarray(q8.reshape(B, 1, H, D).transpose(0, 2, 1, 3)), k, v, None, qm, qs,
+                           f, am, as_)
+    t16 = (Tk + 15) // 16 * 16
+    vt = np.zeros((B, H, D, t16), np.int8)
+    vt[..., :Tk] = v
+    wf = torch.zeros(iw._lib.value("iw_frag_bytes", C, C), dtype=torch.int8, device="cuda")
+    wt = T(w)
+    iw._lib.call("iw_frag_pack", wt.data_ptr(), C, C, C, wf.data_ptr(), stream())
+    out = torch.zeros(iw._lib.value("iw_frag_bytes", B, C), dtype=torch.int8, device="cuda")
+    xt, gt, bt, kt, vtt = T(x), T(gamma), T(beta), T(k), T(vt)
+    qbt = None if qb is None else T(qb)
+    qzt = None if qz is None else T(qz)
+    qmt, qst = T(qm_), T(qs_)
+    iw._lib.call("iw_attention_decode_cross_lnq", xt.data_ptr(), C, gt.data_ptr(), bt.data_ptr(), lm, ls, om, os_, 13,
+                 True, wf.data_ptr(), None if qbt is None else qbt.data_ptr(),
+                 None if qzt is None else qzt.data_ptr(), qmt.data_ptr(), qst.data_ptr(), bias, asym, kt.data_ptr(),
+                 H * Tk * D, Tk * D, D, vtt.data_ptr(), H * D * t16, D * t16, t16, out.data_ptr(), B, H, D, Tk, qm,
+                 qs, f, am, as_, 16, stream())
+    torch.cuda.synchronize()
+    got = _unfrag(host(out), B, C)
+    assert np.array_equal(got.reshape(B, 1, C), exp)
+
+
+def test_attention_decode_cross_lnq_rejects(iw, gpu):
+    """Unsupported shapes fail with a message and launch nothing."""
+    t = torch.zeros(1 << 16, dtype=torch.int8, device="cuda")
+    p = t.data_ptr()
+    base = dict(heads=20, head_dim=64, k_length=1500, batch=2)
+
+    def call(heads, head_dim, k_length, batch):
+        return iw._lib.call("iw_attention_decode_cross_lnq", p, heads * head_dim, p, None, 1, 1, 1, 1, 13, False, p,
+                            None, None, p, p, False, False, p, 0, 0, 64, p, 0, 0, 1504, p, batch, heads, head_dim,
+                            k_length, 1, 1, 8, 1, 1, 16, stream())
+    for over, what in (({"head_dim": 96}, "head_dim 64"), ({"heads": 7}, "LayerNorm hidden size"),
+                       ({"k_length": 3000}, "keys"), ({"batch": 129}, "rows")):
+        kw = dict(base, **over)
+        with pytest.raises(RuntimeError, match=what):
+            call(**kw)
+
+
+def test_fused_cross_attention_does_not_change_results(iw, gpu, tiny_model):
+    """The one-token step with the cross-attention's LayerNorm and query
+    projection fused into the attention kernel and as separate launches: the
+    same greedy tokens (replayed graphs) and the same logits step by step."""
+    dims, params = tiny_model
+    model = iw.Whisper_int.from_params(dims, params).cuda()
+    B, steps = 5, 19
+    mel = iw.synth.synthetic_mel(B, dims.n_mels, 2 * dims.n_audio_ctx, seed=9)
+    prompt = np.random.default_rng(9).integers(0, dims.n_vocab, size=(B, 3)).astype(np.int64)
+    runners = [iw.DecoderRunner(model.decoder, B, dims.n_audio_ctx, fuse_cross=fc) for fc in (False, True)]
+    eager = [iw.DecoderRunner(model.decoder, B, dims.n_audio_ctx, use_graph=False, fuse_cross=fc)
+             for fc in (False, True)]
+    assert runners[1].fuse_cross and not runners[0].fuse_cross
+    with torch.no_grad():
+        feats = model.embed_audio(T(mel))
+        toks = [host(iw.greedy_decode(model, feats, T(prompt), steps, runner=r)) for r in runners]
+        logits = [host(iw.greedy_decode(model, feats, T(prompt), steps, runner=r, keep_logits=True)[1])
+                  for r in eager]
+    assert np.array_equal(toks[0], toks[1])
+    assert np.array_equal(logits[0], logits[1])
