@@ -11,7 +11,8 @@ audio-s/s, decoder tokens/s, two roofline objects and the CPU oracle timed on a
 bounded sample on the host:
 
 * ``roofline``: the kernel with the largest share of the step, the decoder's
-  cross-attention over the cached audio K/V (HBM-bound, ``XA_KERNEL``). Its launches inside
+  cross-attention over the cached audio K/V with its LayerNorm and query
+  projection computed in the kernel (HBM-bound, ``XA_KERNEL``). Its launches inside
   the timed steps run in a replayed HIP graph, so its duration is taken right
   after the timed region from launches identical to the graph's (same kernel,
   same buffers, same stream) bracketed by HIP events on that stream.
@@ -140,9 +141,10 @@ PMC_SUMMARIES = (ROOT / "profiles" / "attn_decode_cross_b128_pmc.md",
                  ROOT / "profiles" / "encoder_mfma_large_b128_pmc.md",
                  ROOT / "profiles" / "large_b128_step_kernel_stats.md")
 GEMM_TRAFFIC_KEY = "gemm_dtl_kernel (encoder layer average)"
-# the decoder cross-attention kernel as profilers name it (key capacity, ring
-# slots, keys per chunk, waves per (batch, head))
-XA_KERNEL = "attn_decode_stream_kernel<2048, 3, 128, 4>"
+# the decoder cross-attention kernel of the token step as profilers name it
+# (the one that also computes the LayerNorm and query before it)
+XA_KERNEL = "attn_decode_cross_lnq_kernel"
+XA_KERNEL_PLAIN = "attn_decode_stream_kernel<2048, 3, 128, 4>"
 
 
 def recorded(key: str, kernel: str):
@@ -165,19 +167,25 @@ def recorded_traffic(kernel: str):
 
 
 def cross_attention_probe(dec, dims, batch: int, launches: int = 20) -> float:
-    """Average duration (ms) of the decoder cross-attention kernel on layer 0's
-    cached K/V, HIP events on the launch stream around each launch."""
+    """Average duration (ms) of the token step's cross-attention kernel (with
+    its LayerNorm and query projection) on layer 0's cached K/V and the last
+    step's residual rows, HIP events on the launch stream around each launch."""
     import torch
 
-    C = dims.n_text_state
-    q = torch.randint(-127, 128, (batch, C), dtype=torch.int8, device="cuda")
-    out = torch.empty((batch, C), dtype=torch.int8, device="cuda")
-    dec.cross_attention(0, q, out)  # warm
+    if dec.fuse_cross:
+        out = torch.empty_like(dec.wvf)
+        launch = lambda: dec.cross_attention_lnq(0, out)
+    else:  # head sizes other than 64: the plain kernel on a random query
+        C = dims.n_text_state
+        q = torch.randint(-127, 128, (batch, C), dtype=torch.int8, device="cuda")
+        out = torch.empty((batch, C), dtype=torch.int8, device="cuda")
+        launch = lambda: dec.cross_attention(0, q, out)
+    launch()  # warm
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(launches)]
     for e0, e1 in ev:
         e0.record()
-        dec.cross_attention(0, q, out)
+        launch()
         e1.record()
     torch.cuda.synchronize()
     return sum(e0.elapsed_time(e1) for e0, e1 in ev) / launches
@@ -323,6 +331,7 @@ def main():
         wall = time.perf_counter() - t_start
         if dsteps:
             xa_ms = cross_attention_probe(dec, dims, batch)
+            dec_fused = dec.fuse_cross
         rowops = rowop_bandwidth(iw, batch * dims.n_audio_ctx, dims.n_audio_state, batch, dims.n_audio_ctx)
     enc_ms = sum(e0.elapsed_time(e1) for e0, e1, _, _ in evs)
     dec_ms = sum(e1.elapsed_time(e2) for _, e1, e2, _ in evs)
@@ -373,14 +382,20 @@ def main():
         "hbm_kernels": rowops,
     }
     if dsteps:
-        # algorithmic bytes: K [Tk, D] and V [D, Tk] of every (b, h), q and out
+        # algorithmic bytes: K [Tk, D] and V [D, Tk] of every (b, h), the
+        # residual rows (int16) and the query weight read once, and out
         H, D, Tk = dims.n_text_head, dims.n_text_state // dims.n_text_head, dims.n_audio_ctx
-        xa_bytes = batch * H * (2 * Tk * D + 2 * D)
+        C = H * D
+        if dec_fused:
+            xa_bytes = batch * H * 2 * Tk * D + batch * C * 2 + C * C + batch * C
+        else:  # K, V, q and out
+            xa_bytes = batch * H * (2 * Tk * D + 2 * D)
         xa_gbs = xa_bytes / (xa_ms * 1e-3) / 1e9
-        kname = XA_KERNEL
+        kname = XA_KERNEL if dec_fused else XA_KERNEL_PLAIN
         result["roofline"] = {
-            "bound": "hbm", "kernel": kname + " (decoder cross-attention, 1 query x "
-                     f"{Tk} cached keys per (batch, head))",
+            "bound": "hbm", "kernel": kname + " (decoder cross-attention"
+                     + (" with its LayerNorm and query projection" if dec_fused else "")
+                     + f", 1 query x {Tk} cached keys per (batch, head))",
             "achieved": round(xa_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(xa_gbs / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(kname),
             "bytes_per_launch": xa_bytes, "avg_launch_ms": round(xa_ms, 4),

@@ -471,6 +471,28 @@ class DecoderRunner:
         att = self.dec.blocks[layer].cross_attn
         self._cross_attend(att, layer, q.data_ptr(), self.C, self.C, 1, out, None)
 
+    def cross_attention_lnq(self, layer: int, out: torch.Tensor):
+        """The one-token step's fused cross-attention of ``layer`` (its
+        LayerNorm and query projection computed in the kernel) on the current
+        residual rows (``x16``): out is the fragment-major [B, C] image (launched
+        on the current stream; needs ``fuse_cross``)."""
+        if not self.fuse_cross:
+            raise ValueError("this runner does not fuse the cross-attention")
+        self._cross_lnq(layer, out)
+
+    def _cross_lnq(self, l: int, out: torch.Tensor):
+        blk = self.dec.blocks[l]
+        B, C, H, D, Ta = self.B, self.C, self.H, self.D, self.Ta
+        s = blk.cross_attn._scalars()
+        ln, cq = blk.cross_attn_ln, self.f_cq[l]
+        lsc = ln._scalars()
+        _lib.call("iw_attention_decode_cross_lnq", self.x16.data_ptr(), C, ln.weight.data_ptr(), _ptr(ln.bias),
+                  lsc["lm"], lsc["ls"], lsc["om"], lsc["os"], ln.offset, ln.bias is not None,
+                  cq.w.data_ptr(), _ptr(cq.bias), _ptr(cq.wz), cq.mult.data_ptr(), cq.shift.data_ptr(),
+                  cq.bias is not None, cq.wz is not None, self.k_cross[l].data_ptr(), H * Ta * D, Ta * D, D,
+                  self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16, out.data_ptr(), B, H,
+                  D, Ta, s["qm"], s["qs"], s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
+
     def _finish(self, x_last: torch.Tensor, pos_inc: int):
         """Final LayerNorm of the last position, classifier (with the row maxima
         fused into its epilogue on the fragment-major path), then one
@@ -637,15 +659,7 @@ class DecoderRunner:
             s = blk.cross_attn._scalars()
             Ta = self.Ta
             if self.fuse_cross:
-                ln, cq = blk.cross_attn_ln, self.f_cq[l]
-                lsc = ln._scalars()
-                _lib.call("iw_attention_decode_cross_lnq", x16.data_ptr(), C, ln.weight.data_ptr(), _ptr(ln.bias),
-                          lsc["lm"], lsc["ls"], lsc["om"], lsc["os"], ln.offset, ln.bias is not None,
-                          cq.w.data_ptr(), _ptr(cq.bias), _ptr(cq.wz), cq.mult.data_ptr(), cq.shift.data_ptr(),
-                          cq.bias is not None, cq.wz is not None, self.k_cross[l].data_ptr(), H * Ta * D,
-                          Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16, D * self.ta16, self.ta16,
-                          wvf.data_ptr(), B, H, D, Ta, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
-                          blk.cross_attn.rsqrt_offset, _stream())
+                self._cross_lnq(l, wvf)
             else:
                 _ln_frag(blk.cross_attn_ln, x16, B, h8f, pf(self.f_cq[l]))
                 self.f_cq[l].linear8(h8f, B, q8)
