@@ -1058,8 +1058,11 @@ __device__ __forceinline__ void attn_decode_stream_body(const AttnArgs &a, const
   }
   LnqRegs lr;
   if constexpr (LNQ) ln_query_load(lq, b, h, lr);
+  // LNQ: the last slot holds no copied query, so chunk NR - 1 is copied now
+  // too, during the LayerNorm and projection (the loop then issues chunk
+  // i + NR - 1 from i = 1 on; at i = 0 its wait also covers chunk 1)
 #pragma unroll
-  for (int i = 0; i < NR - 1; ++i)
+  for (int i = 0; i < (LNQ ? NR : NR - 1); ++i)
     if (i < T) issue(i);
   const int8_t *q8 = nullptr;
   if constexpr (LNQ) q8 = ln_query(lq, lr, h, sP);
@@ -1144,7 +1147,7 @@ __device__ __forceinline__ void attn_decode_stream_body(const AttnArgs &a, const
     for (int u = 0; u < DPC; ++u)
       x[u] = *reinterpret_cast<const v4i *>(sRing + (i % NR) * SLOT + wave * WB + u * 1024 + lane * 16);
     // the slot of chunk i - 1 is free: this wave read it last iteration
-    if (i + NR - 1 < T) issue(i + NR - 1);
+    if (i + NR - 1 < T && (!LNQ || i > 0)) issue(i + NR - 1);
     if (i < nK) {
 #pragma unroll
       for (int u = 0; u < DPC; ++u) {
