@@ -80,7 +80,7 @@ SIGNATURES = {
                                       _u8, _i8, _i32, _u8, _i8, _u32, _p],
     "iw_attention_decode_cache_frag": [_p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p,
                                        _i64, _i64, _i64, _i64, _p, _i64, _u8, _i8, _i32, _u8, _i8, _u32,
-                                       _p],
+                                       _p, _i64, _i64, _p],
     "iw_classifier_frag": [_p, _p, _u32, _i8, _p, _i64, _i64, _i64, _p],
 }
 

@@ -139,7 +139,8 @@ int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k,
                                  int64_t head_dim,
                                  int64_t k_length, const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                                  int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
-                                 uint32_t rsqrt_offset, bool out_frag, iw_stream_t stream) {
+                                 uint32_t rsqrt_offset, bool out_frag, iw_stream_t stream,
+                                 const FragPrefetch *tail = nullptr) {
   IW_REQUIRE(frac_bits > 0 && frac_bits < 14, "frac_bits must be in [1, 14)");
   IW_REQUIRE(rsqrt_offset <= 29, "rsqrt_offset must be in [0,29]");
   IW_REQUIRE(head_dim == 64 || head_dim == 96 || head_dim == 128,
@@ -195,7 +196,7 @@ int attention_decode_cache_entry(const int8_t *q, int64_t q_sb, const int8_t *k,
                "a fragment-major attention output takes at most 128 rows of 5120 channels");
     a.o_frag_kp = frag_kpad(heads * head_dim);
   }
-  return launch_attn_decode_cache(a, pos, as_stream(stream));
+  return launch_attn_decode_cache(a, pos, as_stream(stream), tail);
 }
 
 // Fragment-major operands: sizes the kernels take and 16-byte alignment.
@@ -951,11 +952,14 @@ int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *
                                    int64_t v_sq, int8_t *out, int64_t batch, int64_t heads, int64_t head_dim,
                                    int64_t k_length, const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                                    int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier, int8_t av_shift,
-                                   uint32_t rsqrt_offset, iw_stream_t stream) {
+                                   uint32_t rsqrt_offset, const int8_t *next_weight, int64_t next_n,
+                                   int64_t next_k, iw_stream_t stream) {
+  FragPrefetch pf;
+  const int rc = frag_prefetch_args(next_weight, next_n, next_k, &pf);
+  if (rc) return rc;
   return attention_decode_cache_entry(q, q_sb, k, k_sb, k_sh, k_st, vt, v_sb, v_sh, v_sd, v_sq, out, 0, batch,
-                                      heads,
-                                      head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
-                                      av_multiplier, av_shift, rsqrt_offset, true, stream);
+                                      heads, head_dim, k_length, pos, max_keys, qk_multiplier, qk_shift, frac_bits,
+                                      av_multiplier, av_shift, rsqrt_offset, true, stream, &pf);
 }
 
 int iw_attention_decode_cross_lnq(const int16_t *x, int64_t x_ld, const int8_t *ln_weight, const int32_t *ln_bias,

@@ -826,6 +826,10 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 #ifndef IW_DSELF_NW
 #define IW_DSELF_NW 4
 #endif
+// blocks at the end of the self-attention launch that read the next GEMM's
+// weight into L2 (the rest of the launch's K/V stream, which would evict
+// those lines, is short by then)
+constexpr int kSelfTailBlocks = 256;
 
 // The query of (batch b, head h) for attn_decode_cross_lnq_kernel, as 64
 // bytes of LDS: LayerNorm32 of row b (the integer steps of
@@ -1324,7 +1328,7 @@ __device__ __forceinline__ void self_decode_store(const AttnArgs &a, int64_t b, 
 
 template <int NW, int NC>
 __device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, int h, int Tk,
-                                                 SelfDecodeLds<NW> &sm) {
+                                                 SelfDecodeLds<NW> &sm, const FragPrefetch &pf, int pf_start) {
   constexpr int CK = 16 * NW;       // keys per chunk
   constexpr int NG = (NC + 3) / 4;  // scores per lane after the regrouping
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1356,6 +1360,9 @@ __device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, i
   // every load is issued before the first wait (the scheduler would
   // otherwise defer the V loads to reuse registers)
   __builtin_amdgcn_sched_barrier(0);
+  // the launch's last blocks read the out-projection's weight into L2
+  uint32_t pfv[1];  // one line per thread: 8192 per XCD from 256 blocks
+  frag_prefetch_issue_tail(pf, pf_start, kb, pfv);
 
   int32_t dot[NC];
 #pragma unroll
@@ -1444,32 +1451,34 @@ __device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, i
     }
     self_decode_store<NW>(a, b, h, pv, total, tid);
   }
+  frag_prefetch_keep(pfv);
 }
 
 template <int NW, int NC>
 __device__ __forceinline__ void self_decode_dispatch(int nc, const AttnArgs &a, int64_t b, int h, int Tk,
-                                                     SelfDecodeLds<NW> &sm) {
+                                                     SelfDecodeLds<NW> &sm, const FragPrefetch &pf, int pf_start) {
   if constexpr (NC == 0) {
     // no keys: every sum is 0
     if (threadIdx.x < 64) self_decode_store<NW>(a, b, h, 0u, 0u, threadIdx.x);
   } else {
     if (nc == NC)
-      self_decode_body<NW, NC>(a, b, h, Tk, sm);
+      self_decode_body<NW, NC>(a, b, h, Tk, sm, pf, pf_start);
     else
-      self_decode_dispatch<NW, NC - 1>(nc, a, b, h, Tk, sm);
+      self_decode_dispatch<NW, NC - 1>(nc, a, b, h, Tk, sm, pf, pf_start);
   }
 }
 
 // at most 16 NW NCMAX keys
 template <int NW, int NCMAX>
-__global__ __launch_bounds__(64 * NW) void attn_decode_self_kernel(AttnArgs a, const int32_t *pos) {
+__global__ __launch_bounds__(64 * NW) void attn_decode_self_kernel(AttnArgs a, const int32_t *pos, FragPrefetch pf,
+                                                                    int pf_start) {
   __shared__ __attribute__((aligned(16))) SelfDecodeLds<NW> sm;
   const int64_t bh = blockIdx.x;
   const int h = (int)(bh % a.H);
   const int64_t b = bh / a.H;
   const int Tk = min(a.Tk + (pos ? *pos : 0), a.max_tk);
   const int nc = (Tk + 16 * NW - 1) / (16 * NW);
-  self_decode_dispatch<NW, NCMAX>(nc, a, b, h, Tk, sm);
+  self_decode_dispatch<NW, NCMAX>(nc, a, b, h, Tk, sm, pf, pf_start);
 }
 
 }  // namespace
@@ -1533,6 +1542,13 @@ int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s) {
   return check_launch("attn_prefill_kernel");
 }
 
+// the blocks blockIdx >= the returned start (a multiple of 8) of a grid of g
+// blocks: the last `tail` of them, rounded up to whole XCD rounds
+static int tail_start(int64_t g, int tail) {
+  const int64_t st = g > tail ? (g - tail) / 8 * 8 : 0;
+  return (int)st;
+}
+
 int launch_attn_decode_cross_lnq(const AttnArgs &a, const LnQueryArgs &lq, hipStream_t s) {
   if ((int64_t)a.B * a.H == 0) return 0;
   const uintptr_t al = reinterpret_cast<uintptr_t>(a.k) | reinterpret_cast<uintptr_t>(a.vt) | (uintptr_t)a.k_st |
@@ -1545,7 +1561,7 @@ int launch_attn_decode_cross_lnq(const AttnArgs &a, const LnQueryArgs &lq, hipSt
   return check_launch("attn_decode_cross_lnq_kernel");
 }
 
-int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s) {
+int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s, const FragPrefetch *tail) {
   if ((int64_t)a.B * a.H == 0) return 0;
   // a set is one 16-key chunk of V^T per lane, 1024 keys per wave; up to two
   // sets are loaded into registers before the scores are computed
@@ -1573,16 +1589,24 @@ int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t 
     // (32-bit offsets inside a head's K rows and V quads)
     const bool off32 = (int64_t)a.max_tk * a.k_st < (1ll << 31) && (int64_t)(a.max_tk + 3) / 4 * a.v_sq < (1ll << 31);
     if (vq && a.max_tk <= 16 * IW_DSELF_NW * 8 && off32) {
-      // self-attention caches: every load in flight at once
+      // self-attention caches: every load in flight at once; the last
+      // kSelfTailBlocks blocks read the next GEMM's weight into L2
+      FragPrefetch tpf = tail ? *tail : FragPrefetch();
+      const int tstart = tail_start(grid.x, kSelfTailBlocks);
+      frag_prefetch_launch(tpf, grid.x - tstart, 64 * IW_DSELF_NW);
       const int ncmax = (a.max_tk + 16 * IW_DSELF_NW - 1) / (16 * IW_DSELF_NW);
       if (ncmax <= 2)
-        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 2>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 2>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos,
+                           tpf, tstart);
       else if (ncmax <= 4)
-        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 4>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 4>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos,
+                           tpf, tstart);
       else if (ncmax <= 7)
-        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 7>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 7>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos,
+                           tpf, tstart);
       else
-        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 8>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos);
+        hipLaunchKernelGGL((attn_decode_self_kernel<IW_DSELF_NW, 8>), grid, dim3(64 * IW_DSELF_NW), 0, s, a, pos,
+                           tpf, tstart);
       return check_launch("attn_decode_self_kernel");
     }
     if (vq) {

@@ -140,10 +140,13 @@ inline void frag_prefetch_launch(FragPrefetch &p, int64_t blocks, int threads) {
 // address the kernel reads anyway). Pass v to frag_prefetch_keep at the end.
 // The launch geometry comes from p (kernel arguments), not from the
 // dispatch packet, whose read would be a vector-memory wait of its own.
+// blk: this block's index among the launch's prefetching blocks (blockIdx
+// less a multiple of 8, so that blk % 8 is still its XCD); none when !part.
 template <int NL>
-__device__ inline void frag_prefetch_issue(const FragPrefetch &p, const void *fallback, uint32_t (&v)[NL]) {
-  const int blk = (int)blockIdx.x, xcd = blk & 7;
-  const bool on = p.w != nullptr && p.tiles > xcd;
+__device__ inline void frag_prefetch_issue_at(const FragPrefetch &p, int blk, bool part, const void *fallback,
+                                              uint32_t (&v)[NL]) {
+  const int xcd = blk & 7;
+  const bool on = part && p.w != nullptr && p.tiles > xcd;
   const uint32_t per = ((uint32_t)p.blocks - (uint32_t)xcd + 7) >> 3;      // this launch's blocks on the XCD
   const uint32_t ntx = on ? ((uint32_t)p.tiles - (uint32_t)xcd + 7) >> 3 : 0;  // the next GEMM's tiles on it
   const uint32_t tb = (uint32_t)p.tile_bytes;                              // < 2^31 (host-checked)
@@ -166,6 +169,21 @@ __device__ inline void frag_prefetch_issue(const FragPrefetch &p, const void *fa
     t += dq;
     if (c >= lpt) c -= lpt, ++t;
   }
+}
+
+template <int NL>
+__device__ inline void frag_prefetch_issue(const FragPrefetch &p, const void *fallback, uint32_t (&v)[NL]) {
+  frag_prefetch_issue_at(p, (int)blockIdx.x, true, fallback, v);
+}
+
+// The same from the blocks blockIdx >= start (a multiple of 8) of the launch
+// only, with p.blocks the number of those blocks: the last blocks of a long
+// kernel read the next GEMM's weight into L2 shortly before it runs.
+template <int NL>
+__device__ inline void frag_prefetch_issue_tail(const FragPrefetch &p, int start, const void *fallback,
+                                                uint32_t (&v)[NL]) {
+  const int blk = (int)blockIdx.x - start;
+  frag_prefetch_issue_at(p, blk < 0 ? 0 : blk, blk >= 0, fallback, v);
 }
 
 template <int NL>

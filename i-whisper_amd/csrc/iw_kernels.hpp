@@ -141,7 +141,10 @@ int launch_attn_decode(const AttnArgs &a, hipStream_t s);
 // Decode attention over [B,H,T_cap,D] / [B,H,D,T_cap16] caches; key count
 // a.Tk + *pos (pos may be null). At most 4096 keys.
 constexpr int kDecodeCacheMaxKeys = 4096;
-int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s);
+// tail: the next GEMM's weight, read into L2 by the self-attention kernel's
+// last blocks (V in key quads, at most 512 keys), or null
+int launch_attn_decode_cache(const AttnArgs &a, const int32_t *pos, hipStream_t s,
+                             const FragPrefetch *tail = nullptr);
 // Decode cross-attention (one query per (batch, head), keys 0 .. a.Tk - 1,
 // V transposed, head_dim 64) whose query the kernel computes itself from
 // lq; a.q unused. a.o_frag_kp as for launch_attn_decode_cache.

@@ -654,7 +654,7 @@ class DecoderRunner:
                       H * self.Tcap * D, self.Tcap * D, D, self.v_self[l].data_ptr(), *self.v_strides,
                       wvf.data_ptr(), B, H, D, 1,
                       self.pos.data_ptr(), self.Tcap, s["qm"], s["qs"], s["f"], s["am"], s["as_"],
-                      blk.attn.rsqrt_offset, _stream())
+                      blk.attn.rsqrt_offset, *_pf_args(pf(self.f_out[l])), _stream())
             self.f_out[l].linear32_res(wvf, B, x16, sc["a"])
             s = blk.cross_attn._scalars()
             Ta = self.Ta
@@ -666,7 +666,7 @@ class DecoderRunner:
                 _lib.call("iw_attention_decode_cache_frag", q8.data_ptr(), C, self.k_cross[l].data_ptr(),
                           H * Ta * D, Ta * D, D, self.vt_cross[l].data_ptr(), H * D * self.ta16,
                           D * self.ta16, self.ta16, 4, wvf.data_ptr(), B, H, D, Ta, None, Ta, s["qm"], s["qs"],
-                          s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, _stream())
+                          s["f"], s["am"], s["as_"], blk.cross_attn.rsqrt_offset, *_NO_PREFETCH, _stream())
             self.f_co[l].linear32_res(wvf, B, x16, sc["c"])
             f1, f2 = self.f_fc1[l], self.f_fc2[l]
             _ln_frag(blk.mlp_ln, x16, B, h8f, pf(f1))

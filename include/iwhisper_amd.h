@@ -427,14 +427,20 @@ int iw_layernorm32_frag(const int16_t *x, const int8_t *weight, const int32_t *b
                         int64_t next_k, iw_stream_t stream);
 
 /* iw_attention_decode_cache writing the fragment-major image of out
- * [batch][heads*head_dim] (batch <= 128, heads*head_dim <= 5120). */
+ * [batch][heads*head_dim] (batch <= 128, heads*head_dim <= 5120).
+ * next_weight / next_n / next_k (NULL, 0, 0 for none): the fragment-major
+ * weight of the GEMM that runs next, which the launch's last blocks read
+ * into the L2 of the XCD that reads each of its 32-column tiles (a hint, as
+ * for iw_layernorm32_frag; taken by the self-attention kernel: V in key
+ * quads, at most 512 keys). */
 int iw_attention_decode_cache_frag(const int8_t *q, int64_t q_sb, const int8_t *k, int64_t k_sb,
                                    int64_t k_sh, int64_t k_st, const int8_t *vt, int64_t v_sb,
                                    int64_t v_sh, int64_t v_sd, int64_t v_sq, int8_t *out,
                                    int64_t batch, int64_t heads, int64_t head_dim, int64_t k_length,
                                    const int32_t *pos, int64_t max_keys, uint8_t qk_multiplier,
                                    int8_t qk_shift, int32_t frac_bits, uint8_t av_multiplier,
-                                   int8_t av_shift, uint32_t rsqrt_offset, iw_stream_t stream);
+                                   int8_t av_shift, uint32_t rsqrt_offset, const int8_t *next_weight,
+                                   int64_t next_n, int64_t next_k, iw_stream_t stream);
 
 /* iw_classifier with x and weight fragment-major (M <= 128, K <= 5120); out
  * row-major [M][N]. */

@@ -211,7 +211,8 @@ def test_attention_decode_cache_frag(iw, oracle, gpu, B, H, D, Tk, tcap, k_lengt
     of = zeros_frag(iw, B, H * D)
     iw._lib.call("iw_attention_decode_cache_frag", qt.data_ptr(), H * D, kt.data_ptr(), H * tcap * D, tcap * D,
                  D, vt.data_ptr(), *vs, of.data_ptr(), B, H, D, k_length,
-                 None if pos is None else pos.data_ptr(), max_keys, qm, qs, f, am, as_, 16, stream())
+                 None if pos is None else pos.data_ptr(), max_keys, qm, qs, f, am, as_, 16, None, 0, 0,
+                 stream())
     torch.cuda.synchronize()
     assert np.array_equal(host(of), frag_image(exp))
 
