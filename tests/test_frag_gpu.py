@@ -217,6 +217,32 @@ def test_attention_decode_cache_frag(iw, oracle, gpu, B, H, D, Tk, tcap, k_lengt
     assert np.array_equal(host(of), frag_image(exp))
 
 
+@pytest.mark.parametrize("B,H,Tk,next_n,next_k", [(2, 3, 17, 64, 192), (128, 20, 301, 1280, 1280),
+                                                  (128, 20, 448, 1280, 1280), (7, 4, 5, 96, 256)])
+def test_attention_decode_cache_frag_prefetch_hint(iw, oracle, gpu, B, H, Tk, next_n, next_k):
+    """The self-attention kernel's last blocks read a next-GEMM weight into L2:
+    a hint that changes no result (grids smaller and larger than the tail,
+    weights of fewer column tiles than XCDs and of many)."""
+    print("case: decode cache frag prefetch", B, H, Tk, next_n, next_k, flush=True)
+    D, tcap = 64, 448
+    q, k, v, qm, qs, f, am, as_ = gen.attn_case(11 * B + Tk, B, H, 1, Tk, D)
+    exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_).reshape(B, H * D)
+    kc = np.zeros((B, H, tcap, D), np.int8)
+    shape, vs = gen.v_cache_layout(B, H, D, tcap, "quads")
+    vc = np.zeros(shape, np.int8)
+    kc[:, :, :Tk] = k
+    gen.v_cache_put(vc, "quads", 0, v)
+    qt, kt, vt = T(q.reshape(B, H * D)), T(kc), T(vc)
+    wn = pack(iw, gen.i8(gen.rng(B + Tk), (next_n, next_k)))
+    for hint in ((None, 0, 0), (wn.data_ptr(), next_n, next_k)):
+        of = zeros_frag(iw, B, H * D)
+        iw._lib.call("iw_attention_decode_cache_frag", qt.data_ptr(), H * D, kt.data_ptr(), H * tcap * D,
+                     tcap * D, D, vt.data_ptr(), *vs, of.data_ptr(), B, H, D, Tk, None, Tk, qm, qs, f, am, as_,
+                     16, *hint, stream())
+        torch.cuda.synchronize()
+        assert np.array_equal(host(of), frag_image(exp))
+
+
 @pytest.mark.parametrize("B,H,D,pos_val,tcap", [(128, 20, 64, 100, 448), (5, 6, 64, 447, 448),
                                                 (3, 4, 96, 0, 448), (2, 2, 64, 40, 40)])
 @pytest.mark.parametrize("layout", gen.V_LAYOUTS)
