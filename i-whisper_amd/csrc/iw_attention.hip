@@ -829,7 +829,7 @@ __global__ __launch_bounds__(256) void attn_decode_cache_kernel(AttnArgs a, cons
 // blocks at the end of the self-attention launch that read the next GEMM's
 // weight into L2 (the rest of the launch's K/V stream, which would evict
 // those lines, is short by then)
-constexpr int kSelfTailBlocks = 256;
+constexpr int kSelfTailBlocks = 128;
 
 // The query of (batch b, head h) for attn_decode_cross_lnq_kernel, as 64
 // bytes of LDS: LayerNorm32 of row b (the integer steps of
@@ -1361,7 +1361,7 @@ __device__ __forceinline__ void self_decode_body(const AttnArgs &a, int64_t b, i
   // otherwise defer the V loads to reuse registers)
   __builtin_amdgcn_sched_barrier(0);
   // the launch's last blocks read the out-projection's weight into L2
-  uint32_t pfv[1];  // one line per thread: 8192 per XCD from 256 blocks
+  uint32_t pfv[1];  // one line per thread: 4096 per XCD from 128 blocks
   frag_prefetch_issue_tail(pf, pf_start, kb, pfv);
 
   int32_t dot[NC];
