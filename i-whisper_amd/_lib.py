@@ -10,6 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libiwhisper_amd.so"
+ABI_VERSION = 2  # IW_ABI_VERSION of include/iwhisper_amd.h that SIGNATURES describe
 
 _p = C.c_void_p
 _i64 = C.c_int64
@@ -117,6 +118,10 @@ def load() -> C.CDLL:
             lib.iw_last_error.restype = C.c_char_p
             lib.iw_last_error.argtypes = []
             lib.iw_abi_version.restype = C.c_int
+            got = lib.iw_abi_version()
+            if got != ABI_VERSION:
+                raise IWError(f"{LIB_PATH} has C ABI version {got}; these bindings need {ABI_VERSION} "
+                              "(rebuild the library)")
             _lib = lib
         return _lib
 

@@ -1001,7 +1001,10 @@ __device__ __forceinline__ void attn_decode_stream_body(const AttnArgs &a, const
   constexpr int NACC = VQ ? 4 : DPC;  // P.V sums per lane
   static_assert(!VQ || NW * 64 * 4 <= MAXK * 2, "the wave sums of P.V fit in the score array");
   static_assert(NQ == 1 || !VQ, "several queries stream V transposed");
-  static_assert(!LNQ || (NQ == 1 && !VQ && NW == 4 && MAXK >= 1280), "the fused query: one, V transposed");
+  static_assert(!LNQ || (NQ == 1 && !VQ && NW == 4), "the fused query: one, V transposed");
+  // the fused query's LayerNorm keeps its normalised row (up to 1280 bytes) and the 64 query
+  // channels' int32 sums (at byte 1280) in sP
+  static_assert(!LNQ || NQ * MAXK >= 1280 + 64 * (int)sizeof(int32_t), "the fused query's row and sums fit in sP");
   __shared__ __attribute__((aligned(1024))) int8_t sRing[NR * SLOT];
   __shared__ __attribute__((aligned(16))) int16_t sS[NQ * MAXK];  // requantized scores
   __shared__ __attribute__((aligned(16))) uint8_t sP[NQ * MAXK];

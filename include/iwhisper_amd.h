@@ -33,7 +33,11 @@ extern "C" {
 #define IW_EINVAL (-1)  /* invalid argument (shape, size, parameter range) */
 #define IW_ELAUNCH (-2) /* HIP runtime error at launch */
 
-#define IW_ABI_VERSION 1
+/* 2: iw_transpose_heads (dst_sq), iw_linear8_qkv_cache[_frag] and iw_attention_decode_cache (v_sq),
+ * iw_attention_decode_cache_frag (v_sq, next-weight prefetch) and iw_greedy_advance_filtered
+ * (sum_logprobs, eot_count) changed their argument lists; a caller built against version 1 must
+ * not bind this library. */
+#define IW_ABI_VERSION 2
 #define IW_SHIFT_EXP_TABLE_BYTES 32768
 
 typedef void *iw_stream_t; /* hipStream_t */

@@ -65,7 +65,7 @@ def test_validation_errors_reach_iw_last_error(iw, lib):
     assert rc != 0
     assert b"unsupported LayerNorm hidden size" in lib.iw_last_error()
     lib.iw_abi_version.restype = ctypes.c_int
-    assert lib.iw_abi_version() >= 1
+    assert lib.iw_abi_version() == iw._lib.ABI_VERSION
 
 
 def test_frag_bytes(iw):

@@ -55,14 +55,16 @@ def _decode_cache(iw, q, k, v, qm, qs, f, am, as_, *, tcap, k_length, pos_val, m
     return host(out).reshape(B, 1, H * D)
 
 
-@pytest.mark.parametrize("B,H,D,Tk,tcap,k_length", [
-    (2, 3, 64, 1, 448, 1), (2, 3, 64, 17, 448, 1), (1, 2, 64, 448, 448, 1), (3, 2, 64, 200, 448, 1),
-    (2, 4, 64, 1500, 1500, 1500), (1, 2, 96, 100, 448, 1), (1, 1, 128, 300, 448, 1),
-    (2, 2, 64, 33, 40, 33)])
-@pytest.mark.parametrize("layout", gen.V_LAYOUTS)
+# V in key quads is read for head_dim 64 only (test_attention_decode_cache_quads_rejects
+# checks the refusal); head_dim 96 and 128 run with V transposed
+_DECODE_CASES = [(2, 3, 64, 1, 448, 1), (2, 3, 64, 17, 448, 1), (1, 2, 64, 448, 448, 1), (3, 2, 64, 200, 448, 1),
+                 (2, 4, 64, 1500, 1500, 1500), (2, 2, 64, 33, 40, 33)]
+
+
+@pytest.mark.parametrize("B,H,D,Tk,tcap,k_length,layout",
+                         [c + (lay,) for c in _DECODE_CASES for lay in gen.V_LAYOUTS]
+                         + [(1, 2, 96, 100, 448, 1, "vt"), (1, 1, 128, 300, 448, 1, "vt")])
 def test_attention_decode_cache(iw, oracle, gpu, B, H, D, Tk, tcap, k_length, layout):
-    if layout != "vt" and D != 64:
-        pytest.skip("V in key quads is read for head_dim 64")
     print("case: decode cache", B, H, D, Tk, tcap, k_length, layout, flush=True)
     q, k, v, qm, qs, f, am, as_ = gen.attn_case(3 * B + Tk + D, B, H, 1, Tk, D)
     exp = oracle.attention(q, k, v, None, qm, qs, f, am, as_)
