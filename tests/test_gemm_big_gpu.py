@@ -151,3 +151,41 @@ def test_conv1d_channels_last_big(iw, oracle, gpu, B, Cin, Tin, Cout, stride):
                  Cout, pe_t.data_ptr(), pm_t.data_ptr(), ps_t.data_ptr(), Cout, Cout,
                  out16.data_ptr(), B, Cin, Tin, Cout, 3, stride, 1, True, stream())
     assert np.array_equal(host(out16), exp16)
+
+
+# The direct-to-LDS GEMM (K % 64 == 0, N % 16 == 0) at shapes with several
+# times more 256 x 256 tiles than the GPU has CUs, ragged M (and N) edges,
+# in-place residual, per-tensor GeLU (the table form) and multipliers on both
+# sides of 2^31.
+@pytest.mark.parametrize("kind,M,K,N", [("l8", 12000, 1280, 3840), ("l8_sym", 12000, 1280, 3840),
+                                        ("l8_bigmult", 12000, 768, 5120), ("gelu_table", 12000, 1280, 5120),
+                                        ("l32res", 20000, 1280, 1040), ("l32res_k5120", 9000, 5120, 1280),
+                                        ("l32", 17000, 512, 2048)])
+def test_gemm_many_tiles(iw, oracle, gpu, kind, M, K, N):
+    print("case: gemm many tiles", kind, M, K, N, flush=True)
+    seed = M + K + N + len(kind)
+    if kind == "l8_bigmult":
+        x, w, b, z, m, s = gen.linear_case(seed, M, K, N, shift_lo=0, shift_hi=40)
+    else:
+        x, w, b, z, m, s = gen.realistic_linear_case(seed, M, K, N, asym=kind != "l8_sym")
+    if kind in ("l8", "l8_sym", "l8_bigmult"):
+        got = iw.kernels.linear8_hip(T(x), T(w), T(b), None if z is None else T(z), T(m), T(s))
+        exp = oracle.linear8(x, w, b, z, m, s)
+    elif kind == "gelu_table":
+        lut, im, is_, om, os_ = gen.gelu_params(gen.rng(seed), N, False, False)
+        got = iw.kernels.linear8_gelu_hip(T(x), T(w), T(b), T(z), T(m), T(s), T(lut), T(im), T(is_), T(om), T(os_))
+        exp = oracle.gelu(oracle.linear8(x, w, b, z, m, s), lut, im, is_, om, os_)
+    elif kind == "l32":
+        got = iw.kernels.linear32_hip(T(x), T(w), T(b), T(z), T(m), T(s))
+        exp = oracle.linear32(x, w, b, z, m, s)
+    else:
+        s[:] = np.arange(N) % 4
+        r = gen.rng(seed + 1)
+        res = r.integers(-16383, 16384, size=(M, N)).astype(np.int16)
+        rm = int(r.integers(1, 65536))
+        exp = oracle.residual15(oracle.linear32(x, w, b, z, m, s), res, rm)
+        got = T(res)
+        iw.kernels.linear32_residual15_hip(T(x), T(w), T(b), T(z), T(m), T(s), got,
+                                           torch.tensor([rm], dtype=torch.uint16), out=got)
+    assert np.array_equal(host(got), exp)
+    assert len(np.unique(exp)) > 100
