@@ -69,47 +69,6 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 1) & 2) | (((r >> 1) ^
 // 128-byte rows (8 chunks): chunk c of row r at position c ^ swz8(r)
 __device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
 
-// Round-half-away-from-zero right shift (the Shift rule) in three operations:
-// the sign term is a one-bit field extract whose width is 0 for a zero shift.
-struct EpiShift {
-  uint32_t half, sh, w;
-  __device__ __forceinline__ void set(uint32_t h, uint32_t s) { half = h, sh = s, w = min(s, 1u); }
-  __device__ __forceinline__ int32_t apply(uint32_t x) const {
-    const uint32_t sgn = (uint32_t)__builtin_amdgcn_sbfe((int32_t)x, 31, w);
-    return (int32_t)(x + half + sgn) >> sh;
-  }
-};
-
-// Per-column requantization operands for one output column.
-struct EpiCol {
-  int32_t m;      // multiplier as int32 (mneg restores the unsigned value)
-  uint32_t mneg;  // all ones when the multiplier is >= 2^31
-  uint32_t half, sh;
-  int32_t nz;     // negated zero point
-  uint32_t b;
-  __device__ __forceinline__ void set(uint32_t mult, uint32_t shift, uint32_t nzp, uint32_t bias) {
-    m = (int32_t)mult, mneg = (uint32_t)((int32_t)mult >> 31), sh = shift, nz = (int32_t)nzp, b = bias;
-  }
-  // acc - wz * rowsum + bias, modulo 2^32 (|wz * rowsum| < 2^31 for K <= 32768)
-  __device__ __forceinline__ uint32_t corrected(int32_t acc, int32_t xsum) const {
-    return (uint32_t)__mul24(nz, xsum) + (uint32_t)acc + b;
-  }
-  // high word of the signed x unsigned 64-bit product
-  __device__ __forceinline__ int32_t mulh(uint32_t x) const {
-    return (int32_t)((uint32_t)__mulhi((int32_t)x, m) + (x & mneg));
-  }
-  // Linear8 / per-tensor int8: clamp(rshift(mulh(corrected), s), -127, 127)
-  __device__ __forceinline__ int32_t requant8(int32_t acc, int32_t xsum) const {
-    const uint32_t hi = (uint32_t)mulh(corrected(acc, xsum));
-    const uint32_t sgn = (uint32_t)__builtin_amdgcn_sbfe((int32_t)hi, 31, min(sh, 1u));
-    return clampi((int32_t)(hi + half + sgn) >> sh, -127, 127);
-  }
-  // Linear32: mulh(corrected) << s
-  __device__ __forceinline__ uint32_t pre_residual(int32_t acc, int32_t xsum) const {
-    return (uint32_t)mulh(corrected(acc, xsum)) << sh;
-  }
-};
-
 // BK: K bytes per stage (64: 3 x 72 KB rings, two blocks per CU; 128: every
 // wave-wide copy reads 8 whole 128-byte lines instead of 16 half lines,
 // 3 x 144 KB, one block per CU)

@@ -189,3 +189,26 @@ def test_gemm_many_tiles(iw, oracle, gpu, kind, M, K, N):
                                            torch.tensor([rm], dtype=torch.uint16), out=got)
     assert np.array_equal(host(got), exp)
     assert len(np.unique(exp)) > 100
+
+
+# Edge shapes of the direct-to-LDS GEMM (K % 64 == 0, N % 16 == 0): a few
+# dozen tiles, the narrowest N, partial 256-column blocks, a short K (four
+# 64-byte steps) and a long one, with and without zero points and with the
+# GeLU table.
+@pytest.mark.parametrize("M,K,N", [(8448, 256, 256), (8269, 1280, 16), (9001, 320, 1040), (8200, 5120, 272),
+                                   (16384 + 129, 768, 2304)])
+@pytest.mark.parametrize("kind", ["asym", "sym", "gelu_table"])
+def test_linear8_dtl_edge_shapes(iw, oracle, gpu, M, K, N, kind):
+    print("case: linear8 dtl edge", kind, M, K, N, flush=True)
+    seed = 3 * M + 5 * K + N + len(kind)
+    x, w, b, z, m, s = gen.realistic_linear_case(seed, M, K, N, asym=kind != "sym")
+    s[: min(4, N)] = [-2, 0, 33, 31][: min(4, N)]
+    if kind == "gelu_table":
+        lut, im, is_, om, os_ = gen.gelu_params(gen.rng(seed), N, False, False)
+        got = iw.kernels.linear8_gelu_hip(T(x), T(w), T(b), T(z), T(m), T(s), T(lut), T(im), T(is_), T(om), T(os_))
+        exp = oracle.gelu(oracle.linear8(x, w, b, z, m, s), lut, im, is_, om, os_)
+    else:
+        got = iw.kernels.linear8_hip(T(x), T(w), T(b), None if z is None else T(z), T(m), T(s))
+        exp = oracle.linear8(x, w, b, z, m, s)
+    assert np.array_equal(host(got), exp)
+    assert len(np.unique(exp)) > (20 if kind == "gelu_table" else 50)
