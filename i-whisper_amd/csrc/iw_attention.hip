@@ -161,7 +161,9 @@ __device__ __forceinline__ int key_row(int kk) {
   return (r >> 2) * 8 + g * 4 + (r & 3);
 }
 
-template <int KS, bool HAS_MASK>
+// DF: the head dim is exactly 32 KS, so whole-chunk K / V^T copies need no
+// bounds tests.
+template <int KS, bool HAS_MASK, bool DF>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 4 : 1)))
 void attn_prefill_kernel(AttnArgs a) {
   constexpr int DP = KS * 32;           // padded head dim
@@ -229,15 +231,26 @@ void attn_prefill_kernel(AttnArgs a) {
     constexpr int KPT = (PF_KC * CPK + 255) / 256;   // K pieces per thread
     constexpr int VPT = (DP * 4 + 255) / 256;        // V^T pieces per thread
     uint4 kv[KPT], vv[VPT];
-    auto load_k = [&](int kc) {
+    // A chunk whose keys are all below Tk (and, with DF, every head dim
+    // valid) is copied without per-piece tests: the tests' zero fills and
+    // exec-mask branches cost more than the loads, and the branchy form made
+    // the compiler wait for the next chunk's loads before this chunk's MFMAs.
+    constexpr bool KWHOLE = DF && (PF_KC * CPK) % 256 == 0;
+    constexpr bool VWHOLE = DF && (DP * 4) % 256 == 0;
+    auto load_k = [&](int kc, auto whole_tag) {
+      constexpr bool W = decltype(whole_tag)::value && KWHOLE;
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
         const int c = tid + 256 * j;
         const int kk = c / CPK, part = c % CPK;
         const int key = kc * PF_KC + kk;
-        kv[j] = make_uint4(0, 0, 0, 0);
-        if (c < PF_KC * CPK && key < a.Tk && part * 16 < D)
+        if (W) {
           kv[j] = *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * a.k_st + part * 16);
+        } else {
+          kv[j] = make_uint4(0, 0, 0, 0);
+          if (c < PF_KC * CPK && key < a.Tk && part * 16 < D)
+            kv[j] = *reinterpret_cast<const uint4 *>(kbase + (int64_t)key * a.k_st + part * 16);
+        }
       }
     };
     auto store_k = [&]() {
@@ -252,15 +265,20 @@ void attn_prefill_kernel(AttnArgs a) {
       }
     };
     // V^T chunk: rows d, 64 keys each (4 pieces of 16 bytes)
-    auto load_v = [&](int kc) {
+    auto load_v = [&](int kc, auto whole_tag) {
+      constexpr bool W = decltype(whole_tag)::value && VWHOLE;
 #pragma unroll
       for (int j = 0; j < VPT; ++j) {
         const int c = tid + 256 * j;
         const int d = c >> 2, part = c & 3;
         const int key0 = kc * PF_KC + part * 16;
-        vv[j] = make_uint4(0, 0, 0, 0);
-        if (c < DP * 4 && d < D && key0 < a.vt_ld)
+        if (W) {
           vv[j] = *reinterpret_cast<const uint4 *>(vbase + (int64_t)d * a.vt_ld + key0);
+        } else {
+          vv[j] = make_uint4(0, 0, 0, 0);
+          if (c < DP * 4 && d < D && key0 < a.vt_ld)
+            vv[j] = *reinterpret_cast<const uint4 *>(vbase + (int64_t)d * a.vt_ld + key0);
+        }
       }
     };
     auto store_v = [&]() {
@@ -286,16 +304,22 @@ void attn_prefill_kernel(AttnArgs a) {
     // The chunks whose keys are all below Tk (no mask) take no per-key test
     // and run as a loop of their own, ahead of the rest.
     int32_t mx = INT32_MIN;
-    auto pass1 = [&](int kc, auto full_tag) {
+    using Yes = std::true_type;
+    using No = std::false_type;
+    // NEXT_WHOLE: chunk kc + 1 exists and all its keys are below Tk
+    auto pass1 = [&](int kc, auto full_tag, auto next_tag) {
       constexpr bool FULL = decltype(full_tag)::value;
+      constexpr bool NEXT_WHOLE = decltype(next_tag)::value;
       store_k();
       __syncthreads();
       // next: K chunk kc + 1, or pass 2's first K and V chunks
-      if (kc + 1 < nkc) {
-        load_k(kc + 1);
+      if (NEXT_WHOLE) {
+        load_k(kc + 1, Yes{});
+      } else if (kc + 1 < nkc) {
+        load_k(kc + 1, No{});
       } else {
-        load_k(0);
-        load_v(0);
+        load_k(0, No{});
+        load_v(0, No{});
       }
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
@@ -316,11 +340,13 @@ void attn_prefill_kernel(AttnArgs a) {
       }
       __syncthreads();
     };
-    load_k(0);
-    const int nfull1 = HAS_MASK ? 0 : a.Tk / PF_KC;
+    load_k(0, No{});
+    // chunks whose keys are all below Tk
+    const int nfk = HAS_MASK ? 0 : a.Tk / PF_KC;
     int kc1 = 0;
-    for (; kc1 < nfull1; ++kc1) pass1(kc1, std::true_type{});
-    for (; kc1 < nkc; ++kc1) pass1(kc1, std::false_type{});
+    for (; kc1 + 1 < nfk; ++kc1) pass1(kc1, Yes{}, Yes{});
+    for (; kc1 < nfk; ++kc1) pass1(kc1, Yes{}, No{});
+    for (; kc1 < nkc; ++kc1) pass1(kc1, No{}, No{});
     mx = max(mx, __shfl_xor(mx, 32));
     const int32_t rowmax = mx == INT32_MIN ? -32768 : qk_requant16(mx, a.qk_m, a.qk_s);
     const uint32_t rmp1 = (uint32_t)(uint16_t)(rowmax + 1);
@@ -362,14 +388,18 @@ void attn_prefill_kernel(AttnArgs a) {
     // the signed int8 MFMA operand as it is. The other chunks keep the
     // per-key tests and the split of P = 128 (x_sub = 0 after the int16 wrap
     // of a row maximum at 32767).
-    auto pass2 = [&](int kc, auto full_tag) {
+    auto pass2 = [&](int kc, auto full_tag, auto next_tag) {
       constexpr bool FULL = decltype(full_tag)::value;
+      constexpr bool NEXT_WHOLE = decltype(next_tag)::value;
       store_k();
       store_v();
       __syncthreads();
-      if (kc + 1 < nkc) {
-        load_k(kc + 1);
-        load_v(kc + 1);
+      if (NEXT_WHOLE) {
+        load_k(kc + 1, Yes{});
+        load_v(kc + 1, Yes{});
+      } else if (kc + 1 < nkc) {
+        load_k(kc + 1, No{});
+        load_v(kc + 1, No{});
       }
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
@@ -447,10 +477,11 @@ void attn_prefill_kernel(AttnArgs a) {
     };
     // the split point is uniform over the wave; every wave of the block runs
     // nkc iterations, so the barriers pair up
-    const int nfull2 = (!HAS_MASK && no_sat) ? a.Tk / PF_KC : 0;
+    const int nfull2 = no_sat ? nfk : 0;
     int kc2 = 0;
-    for (; kc2 < nfull2; ++kc2) pass2(kc2, std::true_type{});
-    for (; kc2 < nkc; ++kc2) pass2(kc2, std::false_type{});
+    for (; kc2 + 1 < nfull2; ++kc2) pass2(kc2, Yes{}, Yes{});
+    for (; kc2 < nfull2; ++kc2) pass2(kc2, Yes{}, No{});
+    for (; kc2 < nkc; ++kc2) pass2(kc2, No{}, No{});
     psum += (uint32_t)__shfl_xor((int)psum, 32);
     if (g == 0) sInv[wave][ql] = fisr((int32_t)psum, a.rsqrt_off);
     __syncthreads();
@@ -1529,11 +1560,13 @@ int launch_attn_prefill(const AttnArgs &a, int max_blocks, hipStream_t s) {
   if (tiles == 0) return 0;
   const unsigned grid = (unsigned)(tiles < max_blocks ? tiles : max_blocks);
   const int ks = (a.D + 31) / 32;
-#define IW_PF(KS_)                                                                          \
-  if (a.mask)                                                                               \
-    hipLaunchKernelGGL((attn_prefill_kernel<KS_, true>), dim3(grid), dim3(256), 0, s, a);   \
-  else                                                                                      \
-    hipLaunchKernelGGL((attn_prefill_kernel<KS_, false>), dim3(grid), dim3(256), 0, s, a);
+#define IW_PF(KS_)                                                                                 \
+  if (a.mask)                                                                                      \
+    hipLaunchKernelGGL((attn_prefill_kernel<KS_, true, false>), dim3(grid), dim3(256), 0, s, a);   \
+  else if (a.D == 32 * (KS_))                                                                      \
+    hipLaunchKernelGGL((attn_prefill_kernel<KS_, false, true>), dim3(grid), dim3(256), 0, s, a);   \
+  else                                                                                             \
+    hipLaunchKernelGGL((attn_prefill_kernel<KS_, false, false>), dim3(grid), dim3(256), 0, s, a);
   switch (ks) {
     case 1: IW_PF(1) break;
     case 2: IW_PF(2) break;
