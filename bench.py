@@ -375,7 +375,7 @@ def main():
             # MFMA pipes' cycles at work, SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x cycles)
             "mfma_busy_pmc": recorded("mfma_busy_pmc", GEMM_TRAFFIC_KEY)},
         "encoder_attention": {
-            "kernel": "attn_prefill_kernel<2, false>", "achieved_tops": round(a_tops, 1),
+            "kernel": "attn_prefill_kernel<2, false, true>", "achieved_tops": round(a_tops, 1),
             "ops": "4*B*H*T^2*D (QK^T and P.V)",
             "mfma_busy_pmc": recorded("mfma_busy_pmc", "attn_prefill_kernel"),
             "valu_busy_pmc": recorded("valu_busy_pmc", "attn_prefill_kernel")},
