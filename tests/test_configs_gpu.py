@@ -23,10 +23,11 @@ the graphs' last-step logits equal the eager last step's.
 Whisper-base runs its full 6-layer encoder. Whisper-small, -medium and -large
 keep their real width, heads, mel bins, vocabulary, audio length, batch and step
 count with 2 encoder + 2 decoder layers, so the oracle finishes in seconds.
-Whisper-small and Whisper-large also run at full depth (12 + 12 and 32 + 32
-layers): there rows of the full batch equal batch-1 runs of the same input at
-every step's int8 logits (the kernels have no cross-row arithmetic), and rows
-are checked against the oracle at full depth.
+Whisper-small, -medium and -large also run at full depth (12 + 12, 24 + 24 and
+32 + 32 layers, medium after its seeded random prompt ids): there rows of the
+full batch equal batch-1 runs of the same input at every step's int8 logits
+(the kernels have no cross-row arithmetic), and rows are checked against the
+oracle at full depth.
 """
 import os
 import time
@@ -154,10 +155,12 @@ def test_workload_rows_match_oracle(iw, gpu, name):
                  feats[rows].cpu().numpy(), tokens, logits, streams)
 
 
-# shape -> (batch, greedy steps, rows checked against batch-1 runs, rows checked against the oracle)
+# shape -> (batch, greedy steps, prompt seed or None, rows checked against batch-1 runs, rows
+# checked against the oracle)
 FULL_DEPTH = {
-    "small": (32, 128, (0, 31), (0, 31)),
-    "large": (128, 445, (0, 77, 127), (77,)),
+    "small": (32, 128, None, (0, 31), (0, 31)),
+    "medium": (64, 224, 4, (0, 41, 63), (41,)),
+    "large": (128, 445, None, (0, 77, 127), (77,)),
 }
 
 
@@ -168,14 +171,14 @@ def test_full_depth(iw, gpu, shape):
     and the oracle rows match at full depth (encoder output, the logits of every
     step, the greedy tokens)."""
     dims = iw.SHAPES[shape]
-    B, steps, batch1_rows, oracle_rows = FULL_DEPTH[shape]
+    B, steps, pseed, batch1_rows, oracle_rows = FULL_DEPTH[shape]
     _log(f"full depth {shape}: {dims.n_audio_layer}+{dims.n_text_layer} layers, batch {B}, {steps} steps")
     t0 = time.time()
     params = iw.synth.calibrated_int_params(dims, seed=0)
     _log(f"  checkpoint {time.time() - t0:.1f} s")
     model = iw.Whisper_int.from_params(dims, params).cuda().eval()
     mel = iw.synth.synthetic_mel(B, dims.n_mels, 2 * dims.n_audio_ctx, seed=1)
-    prompt = torch.from_numpy(iw.synth.prompt_tokens(B, dims.n_vocab)).cuda()
+    prompt = torch.from_numpy(iw.synth.prompt_tokens(B, dims.n_vocab, seed=pseed)).cuda()
     with torch.no_grad():
         feats = iw.EncoderRunner(model.encoder, B)(torch.from_numpy(mel).cuda()).clone()
         toks, lg = _decode_both(iw, model, feats, prompt, steps, B, dims.n_audio_ctx)
