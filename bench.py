@@ -273,9 +273,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=None)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path "
-              f"(--gpus {args.gpus} requested). Data parallelism over the batch is described in "
-              f"DESIGN.md.", file=sys.stderr)
+        print(f"bench.py runs on one GPU: there is no multi-GPU path "
+              f"(--gpus {args.gpus} requested).", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -977,8 +977,8 @@ __device__ __forceinline__ const int8_t *ln_query(const LnQueryArgs &lq, LnqRegs
       rsum += (uint32_t)yo;
     }
   }
-  // the normalised row's sum, for the zero-point term (round 0's words are
-  // free: every thread read them before the second barrier)
+  // the normalised row's sum, for the zero-point term (the first reduction's
+  // words are free: every thread read them before the second barrier)
   rsum = wave_sum_dpp(rsum);
   if (lane == 0) sLn[0][wave] = rsum;
   lds_barrier();

@@ -29,7 +29,7 @@ def _stream() -> int:
 def check_backend(backend: str) -> None:
     if backend not in BACKENDS:
         raise NotImplementedError(
-            f"Backend {backend} is not implemented; this build runs the 'hip' (gfx950) backend")
+            f"Backend {backend} is not implemented; this package runs the 'hip' (gfx950) backend")
 
 
 class LinearBase(nn.Linear):

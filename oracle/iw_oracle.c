@@ -2,8 +2,8 @@
  * CPU oracle for the I-Whisper integer encoder/decoder path.
  *
  * TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py use it as the checker. The product library in
- * i-whisper_amd/ never links or calls it.
+ * cpu_baseline leg of bench.py compare the HIP results with it. The product
+ * library in i-whisper_amd/ never links or calls it.
  *
  * Each function restates the scalar kernel cited above it (paths relative to
  * the reference repository root). Wrapping arithmetic is written on uint32_t /

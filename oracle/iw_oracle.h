@@ -1,9 +1,9 @@
 /*
  * CPU oracle for the I-Whisper integer encoder/decoder path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP path is
- * compared against; it is also timed as the CPU baseline in bench.py. The
- * product (i-whisper_amd/) never links, loads or calls it.
+ * TEST INFRASTRUCTURE ONLY. The tests compare the HIP path against this
+ * library; it is also timed as the CPU baseline in bench.py. The product
+ * (i-whisper_amd/) never links, loads or calls it.
  *
  * Every function restates the reference's scalar kernel named in its comment
  * (paths relative to the reference repository root). All arithmetic that the

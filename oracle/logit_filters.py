@@ -1,6 +1,6 @@
 """CPU restatement of the decoding task's logit filters and greedy update
-(TEST INFRASTRUCTURE ONLY: the checker for the device-side filtered greedy
-step; nothing in the product imports it).
+(TEST INFRASTRUCTURE ONLY: the tests compare the device-side filtered greedy
+step against it; nothing in the product imports it).
 
 Follows i_whisper/decoding.py statement by statement on float32 logits with
 -inf masking:

@@ -1,11 +1,11 @@
 """CPU restatement of the log-mel front end (TEST INFRASTRUCTURE ONLY: the
-checker for iw_log_mel; nothing in the product imports it).
+tests compare iw_log_mel against it; nothing in the product imports it).
 
 Follows i_whisper/audio.py:216-267 call by call with torch on the CPU:
 torch.stft(audio, 512, 160, window=hann_window(512), return_complex=True)
 (centred, reflect padding), |X|^2 without the last frame, filters @ power,
 log10 of the clamp at 1e-10, max(., max - 8), / 4 + 1. The filterbank is
-passed in (the build's restatement of librosa.filters.mel, pinned separately
+passed in (the package's restatement of librosa.filters.mel, pinned separately
 against the reference's shipped filterbanks). ``dft_power`` is an independent
 float64 DFT of the same frames, used to pin the STFT step.
 """

@@ -1,5 +1,6 @@
 """CPU restatement of the word-timestamp kernels (TEST INFRASTRUCTURE ONLY:
-the checker for iw_dtw / iw_median_filter; nothing in the product imports it).
+the tests compare iw_dtw / iw_median_filter against it; nothing in the product
+imports it).
 
   dtw_trace      the cost recurrence of triton_ops.py:13-40 (dtw_kernel) on
                  the natural (unskewed) layout, float32, with its tie order:

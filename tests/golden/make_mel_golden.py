@@ -1,6 +1,6 @@
 """Write tests/golden/mel_filters_n400.npz: the reference's shipped mel filterbanks
 (i_whisper/assets/mel_filters.npz, librosa.filters.mel(sr=16000, n_fft=400,
-n_mels=80 / 128)), the fixed point that pins this build's filterbank
+n_mels=80 / 128)), the fixed point that pins the package's filterbank
 restatement. Run from the repository root where /root/reference exists;
 np.load with allow_pickle=False executes nothing from the file."""
 from pathlib import Path
